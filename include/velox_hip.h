@@ -1,0 +1,281 @@
+/*
+ * velox_hip.h — C ABI of the MI355X (gfx950) speculative-decoding verify path.
+ *
+ * Drop-in boundary for the reference's Metal backend (Soflutionltd/velox,
+ * src/paged/).  Conventions shared by every entry point:
+ *   - returns 0 on success, non-zero on error; the message is available from
+ *     vx_last_error() on the calling thread (the reference's anyhow::bail!);
+ *   - tensors are caller-owned device pointers with explicit sizes, contiguous
+ *     row-major, dtype given by a vx_dtype code; index tensors are uint32;
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream); work
+ *     is enqueued asynchronously and ordered on that stream, like candle's
+ *     command encoder;
+ *   - entry points validate exactly what the reference validates, with the
+ *     same failure conditions.
+ * No torch or HIP types appear in the signatures.
+ */
+#ifndef VELOX_HIP_H
+#define VELOX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum { VX_F32 = 0, VX_F16 = 1, VX_BF16 = 2 } vx_dtype;
+
+const char *vx_last_error(void);
+const char *vx_version(void);
+
+/* ======================================================================== */
+/* Kernel-level operators (src/paged/metal_kernels.rs)                       */
+/* ======================================================================== */
+
+/* Replaces qmm_4bit (metal_kernels.rs:2069-2076; validation :2082-2130).
+ * Y[M,N] = X[M,K] . deq(W)^T (+ bias), MLX int4 affine format:
+ *   qweight [N, K/8] u32 (8 nibbles little-endian), scales/biases [N, K/g],
+ *   w = q * scale + bias;  X, scales, biases, bias, Y share `dtype`.
+ * bias may be NULL.  Split-K scratch comes from a library-owned per-stream
+ * workspace allocated on first use. */
+int vx_qmm_4bit(const void *x, const uint32_t *qweight, const void *scales, const void *biases,
+                const void *bias, void *y, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                int dtype, void *stream);
+
+/* Epilogue variants used by the fused verify forward. */
+typedef enum {
+    VX_EPI_STORE = 0,    /* Y = round_T(acc)                                   */
+    VX_EPI_RESIDUAL = 1, /* Y = round_T(R + round_T(acc)), R [M,N] in y_dtype   */
+    VX_EPI_SWIGLU = 2    /* weights rows interleaved in 16-row blocks gate|up:
+                            Y[m,f] = round_T(round_T(silu(g)) * u), Y [M, N/2] */
+} vx_epilogue;
+
+/* Extended int4 GEMM: X is f16 (any value representable in f16, optionally
+ * holding X_true * 2^-x_shift), scales/biases f16 [N, K/g], accumulation in
+ * f32, result rounded to `round_dtype` semantics and stored as `y_dtype`.
+ * workspace (device, >= vx_qmm_workspace_size bytes, first 64 KiB zeroed
+ * once by the caller and left zero by the kernel) may be NULL to use the
+ * per-stream library workspace. */
+int vx_qmm_4bit_ex(const void *x, const uint32_t *qweight, const void *scales,
+                   const void *biases, void *y, const void *residual, int64_t m, int64_t n,
+                   int64_t k, int64_t group_size, int x_shift, int round_dtype, int y_dtype,
+                   int epilogue, void *workspace, size_t workspace_bytes, void *stream);
+size_t vx_qmm_workspace_size(int64_t m, int64_t n, int64_t k);
+
+/* Replaces paged_prefill_attention (metal_kernels.rs:1680-1690; validation
+ * :1697-1745; kernel MSL :307-395) and, with tree_mask, extends it to tree
+ * verification.  q [total_q, h_q, d]; k_pool/v_pool [P, h_kv, page_size, d];
+ * block_table [n_seqs, max_blocks]; cu_seqlens [n_seqs+1]; seq_id_per_q
+ * [total_q]; kv_offsets [n_seqs]; out [total_q, h_q, d].  tree_mask (device
+ * uint64 [total_q] or NULL): row t of a sequence sees context positions
+ * < kv_offset and tree slot kv_offset + j iff bit j is set; NULL keeps the
+ * reference's causal rule (kv_len = kv_offset + t + 1).  q/k/v/out share
+ * dtype.  Requires head_dim % 32 == 0, head_dim <= 256, h_q % h_kv == 0. */
+int vx_paged_attention(const void *q, const void *k_pool, const void *v_pool,
+                       const uint32_t *block_table, const uint32_t *cu_seqlens,
+                       const uint32_t *seq_id_per_q, const uint32_t *kv_offsets,
+                       const uint64_t *tree_mask, void *out, int64_t total_q, int64_t n_seqs,
+                       int64_t max_blocks, int64_t num_pages, int64_t h_q, int64_t h_kv,
+                       int64_t head_dim, int64_t page_size, float scale, uint32_t sliding_window,
+                       int dtype, void *stream);
+
+/* Replaces paged_decode_attention (metal_kernels.rs:1227-1235; MSL :107-191):
+ * one query row per sequence attending to kv_lens[n] positions. */
+int vx_paged_decode_attention(const void *q, const void *k_pool, const void *v_pool,
+                              const uint32_t *block_table, const uint32_t *kv_lens, void *out,
+                              int64_t n, int64_t max_blocks, int64_t num_pages, int64_t h_q,
+                              int64_t h_kv, int64_t head_dim, int64_t page_size, float scale,
+                              uint32_t sliding_window, int dtype, void *stream);
+
+/* Replaces batched_rope_decode (metal_kernels.rs:1414-1419; MSL :209-241):
+ * in place on x [n, h, d] with per-row offsets[n] into cos/sin [max_pos, d/2]
+ * (same dtype as x). */
+int vx_rope_inplace(void *x, const void *cos_t, const void *sin_t, const uint32_t *offsets,
+                    int64_t n, int64_t h, int64_t d, int64_t max_pos, int dtype, void *stream);
+
+/* Replaces batched_scatter (metal_kernels.rs:1543-1548; MSL :251-279):
+ * pool[page_ids[i], h, slots[i], :] = values[i, h, :]  (exact copy). */
+int vx_kv_scatter(void *pool, const void *values, const uint32_t *page_ids,
+                  const uint32_t *slots, int64_t n, int64_t num_pages, int64_t h,
+                  int64_t page_size, int64_t d, int dtype, void *stream);
+
+/* ======================================================================== */
+/* Acceptance (src/paged/spec.rs:266-301) and its stochastic / tree          */
+/* extensions.  Logits are [rows, vocab] in logits_dtype; outputs are device */
+/* arrays.  `workspace` as for vx_qmm_4bit_ex (NULL = per-stream library     */
+/* workspace).                                                               */
+/* ======================================================================== */
+
+/* argmax_slice (spec.rs:356-366) per row: strict '>', first index wins, NaN
+ * never wins, all -inf/NaN -> 0. */
+int vx_argmax_rows(const void *logits, uint32_t *out, int64_t rows, int64_t vocab,
+                   int logits_dtype, void *stream);
+
+/* Greedy accept + bonus (spec.rs:271-301) for `batch` sequences at once.
+ * logits [batch, k+1, vocab]; candidates [batch, k];
+ * accepted[b] = A; tokens[b, 0..A] = c[0..A) ++ argmax(T[A]). */
+int vx_accept_greedy(const void *logits, const uint32_t *candidates, int32_t *accepted,
+                     uint32_t *tokens, int64_t batch, int64_t k, int64_t vocab,
+                     int logits_dtype, void *stream);
+
+/* Stochastic acceptance (Leviathan et al. 2023 Alg. 1): p = softmax(lt/T),
+ * q = softmax(ld/T); accept c_i iff u_acc < min(1, p(c_i)/q(c_i)); at the
+ * first rejection draw from normalize(max(0, p - q)) with u_res; if all k
+ * are accepted draw the bonus from p_k.  target [batch, k+1, vocab],
+ * draft [batch, k, vocab], uniforms [batch, k+1, 4] f32 (slot 1 = u_acc,
+ * slot 2 = u_res / bonus).  Reductions use a fixed order so decisions are
+ * bit-identical to the host definition. */
+int vx_accept_stochastic(const void *target_logits, const void *draft_logits,
+                         const uint32_t *candidates, const float *uniforms, int32_t *accepted,
+                         uint32_t *tokens, int64_t batch, int64_t k, int64_t vocab,
+                         float temperature, int logits_dtype, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/* Draft-token draw c[b,i] ~ softmax(ld[b,i]/T) with uniforms[b,i,0]. */
+int vx_sample_rows(const void *logits, const float *uniforms, int64_t uniform_stride,
+                   uint32_t *out, int64_t rows, int64_t vocab, float temperature,
+                   int logits_dtype, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Greedy tree acceptance: node 0 is the root (the last committed token);
+ * parents [r] (host array, parents[j] < j); node_tokens [batch, r];
+ * logits [batch, r, vocab].  accepted[b] = path length A; path[b, 0..A]
+ * node indices; tokens[b, 0..A] = tokens of path[1..A] ++ bonus. */
+int vx_accept_tree(const void *logits, const int32_t *parents, const uint32_t *node_tokens,
+                   int32_t *accepted, int32_t *path, uint32_t *tokens, int64_t batch, int64_t r,
+                   int64_t vocab, int logits_dtype, void *stream);
+
+/* ======================================================================== */
+/* Engine level: PagedKvCache (pages.rs), PagedQwen3 (qwen3.rs) and          */
+/* SpecEngine (spec.rs).                                                     */
+/* ======================================================================== */
+
+typedef struct vx_pages vx_pages;
+typedef struct vx_model vx_model;
+typedef struct vx_spec vx_spec;
+
+/* PagedKvConfig + PagedKvCache::new (pages.rs:33-40, :93-136): per-layer K
+ * and V pools [num_pages, kv_heads, page_size, head_dim] in kv_dtype,
+ * zero-initialised; free list pops page 0 first. */
+int vx_pages_create(int64_t layers, int64_t kv_heads, int64_t head_dim, int64_t page_size,
+                    int64_t num_pages, int kv_dtype, vx_pages **out);
+void vx_pages_destroy(vx_pages *p);
+/* PagedKvCache::alloc (pages.rs:173-186): all-or-nothing; returns non-zero
+ * ("not enough free pages") without taking any page. */
+int vx_pages_alloc(vx_pages *p, int64_t n, uint32_t *out_pages);
+/* PagedKvCache::incref_pages / free_pages (pages.rs:192-234). */
+void vx_pages_incref(vx_pages *p, const uint32_t *pages, int64_t n);
+void vx_pages_free(vx_pages *p, const uint32_t *pages, int64_t n);
+int64_t vx_pages_num_free(const vx_pages *p);
+uint32_t vx_pages_refcount(const vx_pages *p, uint32_t page);
+/* layer_k_pool / layer_v_pool (pages.rs:248-254): device pointer. */
+void *vx_pages_pool(vx_pages *p, int64_t layer, int kv);
+
+/* Qwen3Config (qwen3.rs:31-60) subset used by the path. */
+typedef struct {
+    int64_t vocab, hidden, inter, layers, n_heads, n_kv_heads, head_dim;
+    int64_t max_pos, group_size;
+    double rope_theta, rms_eps;
+} vx_qwen3_config;
+
+/* One MLX int4 linear from host memory (qwen3.rs:204-211): qweight u32
+ * [N, K/8]; scales, biases f16 [N, K/g]. */
+typedef struct {
+    const uint32_t *qweight;
+    const uint16_t *scales, *biases;
+} vx_qlinear_host;
+
+typedef struct {
+    const uint16_t *ln1, *ln2, *q_norm, *k_norm; /* f16 [hidden] / [head_dim] */
+    vx_qlinear_host q, k, v, o, gate, up, down;
+} vx_layer_host;
+
+typedef struct {
+    const uint16_t *embed; /* f16 [vocab, hidden] */
+    const vx_layer_host *layers;
+    const uint16_t *norm;
+    vx_qlinear_host lm_head;
+} vx_weights_host;
+
+/* PagedQwen3::load (qwen3.rs:954-986) from host arrays.  Float tensors are
+ * converted to the model dtype (bf16) the way candle's VarBuilder converts
+ * them; KV pages attached later must use kv_dtype f16 or bf16. */
+int vx_model_create(const vx_qwen3_config *cfg, const vx_weights_host *w, int64_t n_layers,
+                    vx_model **out);
+void vx_model_destroy(vx_model *m);
+
+/* SeqSlice (qwen3.rs:254-263): block_table is a host array. */
+typedef struct {
+    int64_t new_tokens, kv_offset;
+    const uint32_t *block_table;
+    int64_t n_blocks;
+} vx_seq_slice;
+
+/* PagedQwen3::forward_all (qwen3.rs:1023-1036) when all_rows != 0, else
+ * PagedQwen3::forward (:994-1017, last row per sequence).  input_ids is a
+ * host array [sum new_tokens]; logits is a device array [rows, vocab] in
+ * bf16.  tree_parents (host, may be NULL): every sequence carries the same
+ * R-node tree (R = new_tokens <= 64), node j written at slot kv_offset + j,
+ * rotated at kv_offset + depth(j), attending to the context and its
+ * ancestors. */
+int vx_forward(vx_model *m, vx_pages *pages, const uint32_t *input_ids,
+               const vx_seq_slice *seqs, int64_t n_seqs, int all_rows,
+               const int32_t *tree_parents, void *logits, void *stream);
+
+/* SpecEngine::new (spec.rs:70-94): rejects vocab / page-size mismatch.
+ * temperature 0 = greedy (the reference's mode); > 0 = stochastic acceptance
+ * with Philox uniforms keyed by sample_seed.  fix_draft_hole = 0 reproduces
+ * spec.rs exactly (c[D-1] never fed to the draft). */
+int vx_spec_create(vx_model *target, vx_pages *target_pages, vx_model *draft,
+                   vx_pages *draft_pages, float temperature, uint64_t sample_seed,
+                   int fix_draft_hole, vx_spec **out);
+void vx_spec_destroy(vx_spec *e);
+
+/* SpecEngine::prefill (spec.rs:131-182) for n prompts (host arrays), batched;
+ * states are numbered 0..n-1 in the returned order (the engine keeps them). */
+int vx_spec_prefill(vx_spec *e, const uint32_t *const *prompts, const int64_t *lens, int64_t n,
+                    int64_t *out_first_state);
+
+/* RoundOutcome (spec.rs:327-335) for one state. */
+typedef struct {
+    int32_t accepted;
+    int32_t n_committed;
+    int32_t stop;
+} vx_round_outcome;
+
+/* SpecEngine::step (spec.rs:186-316) over n states at once (one batched
+ * draft forward per draft position, one batched verify, one acceptance
+ * launch).  committed: host [n, draft_k+1] (row b holds outcome[b].n_committed
+ * tokens).  eos < 0: none.  draft_k == 0 is an error (spec.rs:192-194). */
+int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int64_t draft_k, int64_t eos,
+                 vx_round_outcome *outcomes, uint32_t *committed, void *stream);
+
+/* SpecState accessors (spec.rs:110-124). */
+int64_t vx_spec_state_kv_len(const vx_spec *e, int64_t state);
+int64_t vx_spec_state_num_tokens(const vx_spec *e, int64_t state);
+int vx_spec_state_tokens(const vx_spec *e, int64_t state, uint32_t *out, int64_t cap);
+/* Debug/trace copies of the last step (host): candidates [n, k], verify
+ * logits [n, k+1, vocab] as f32. */
+int vx_spec_last_trace(const vx_spec *e, uint32_t *candidates, float *verify_logits);
+
+/* Per-kernel HIP-event timing of a step (no reference counterpart: the
+ * reference's only timing is Instant around calls, tests/spec_decode.rs).
+ * Classes: 0 = int4 GEMM, 1 = paged attention, 2 = other.  Bytes are
+ * algorithmic (each weight / KV / activation byte counted once). */
+typedef struct {
+    double draft_ms, verify_ms, accept_ms;
+    double verify_kernel_ms[3], verify_kernel_bytes[3];
+    int64_t verify_kernel_launches[3];
+    double draft_kernel_ms[3], draft_kernel_bytes[3];
+    int64_t draft_kernel_launches[3];
+} vx_step_profile;
+int vx_spec_set_profiling(vx_spec *e, int enable);
+int vx_spec_last_profile(const vx_spec *e, vx_step_profile *out);
+
+/* SpecEngine::free (spec.rs:320-323). */
+void vx_spec_free(vx_spec *e, int64_t state);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,68 @@
+"""The C ABI library loads without a GPU, exports every entry point declared in
+include/velox_hip.h, and rejects invalid arguments with the reference's
+messages before touching a device (no compute calls here)."""
+import ctypes as C
+
+import pytest
+
+from velox_amd import _lib
+
+
+def test_every_declared_symbol_is_exported():
+    syms = _lib.header_symbols()
+    assert len(syms) >= 30
+    missing = [s for s in syms if not hasattr(_lib.lib, s)]
+    assert not missing, missing
+    assert _lib.lib.vx_version().decode().startswith("velox_amd")
+
+
+def _err(rc):
+    assert rc != 0
+    return _lib.lib.vx_last_error().decode()
+
+
+def test_qmm_validation_matches_reference():
+    L = _lib.lib
+    # metal_kernels.rs:2084-2097
+    assert "multiple of 8" in _err(L.vx_qmm_4bit(1, 1, 1, 1, None, 1, 2, 4, 12, 64, _lib.F16, None))
+    assert "group_size" in _err(L.vx_qmm_4bit(1, 1, 1, 1, None, 1, 2, 4, 128, 48, _lib.F16, None))
+    assert "group_size" in _err(L.vx_qmm_4bit(1, 1, 1, 1, None, 1, 2, 4, 128, 0, _lib.F16, None))
+    assert "dtype" in _err(L.vx_qmm_4bit(1, 1, 1, 1, None, 1, 2, 4, 128, 64, 7, None))
+
+
+def test_attention_validation_matches_reference():
+    L = _lib.lib
+    # metal_kernels.rs:1702-1711
+    args = [1] * 9
+    assert "divisible" in _err(L.vx_paged_attention(*args, 4, 1, 1, 4, 6, 4, 128, 16, 0.1, 0, _lib.F16, None))
+    assert "D_MAX" in _err(L.vx_paged_attention(*args, 4, 1, 1, 4, 8, 4, 512, 16, 0.1, 0, _lib.F16, None))
+    assert "multiple of 32" in _err(L.vx_paged_attention(*args, 4, 1, 1, 4, 8, 4, 80, 16, 0.1, 0, _lib.F16, None))
+
+
+def test_acceptance_validation():
+    L = _lib.lib
+    assert "draft_k" in _err(L.vx_accept_greedy(1, 1, 1, 1, 2, 0, 10, _lib.BF16, None))
+    bad = (C.c_int32 * 3)(0, 0, 1)
+    assert "root" in _err(L.vx_accept_tree(1, C.cast(bad, C.c_void_p), 1, 1, 1, 1, 1, 3, 10, _lib.BF16, None))
+    fwd = (C.c_int32 * 3)(-1, 2, 1)
+    assert "precede" in _err(L.vx_accept_tree(1, C.cast(fwd, C.c_void_p), 1, 1, 1, 1, 1, 3, 10, _lib.BF16, None))
+    assert "temperature" in _err(L.vx_accept_stochastic(1, 1, 1, 1, 1, 1, 2, 4, 10, 0.0, _lib.F32, None, 0, None))
+
+
+def test_pages_validation():
+    out = C.c_void_p()
+    # pages.rs:94-96
+    assert "page" in _err(_lib.lib.vx_pages_create(2, 4, 8, 4, 0, _lib.F16, C.byref(out)))
+    assert "dtype" in _err(_lib.lib.vx_pages_create(2, 4, 8, 4, 4, _lib.F32, C.byref(out)))
+
+
+def test_no_fallback_when_library_missing(tmp_path, monkeypatch):
+    import importlib.util
+    import shutil
+
+    pkg = tmp_path / "velox_amd"
+    shutil.copytree(_lib.HERE, pkg, ignore=shutil.ignore_patterns("*.so", "_build", "__pycache__", "csrc"))
+    spec = importlib.util.spec_from_file_location("velox_amd_nolib._lib", pkg / "_lib.py")
+    mod = importlib.util.module_from_spec(spec)
+    with pytest.raises(ImportError, match="no CPU fallback"):
+        spec.loader.exec_module(mod)

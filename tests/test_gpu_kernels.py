@@ -1,0 +1,404 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle.
+
+Cases and tolerances follow the reference's own Metal parity tests
+(tests/metal_qmm_4bit_parity.rs, metal_decode_parity.rs,
+metal_batched_kernels_parity.rs) on the same LCG inputs, plus the benchmark
+configs' shapes (config 1 int4 verify GEMMs, config 2 acceptance, config 3 tree
+masks).  Integer outputs (tokens, accept decisions, scatter bytes) must match
+bit-exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+import vxo
+from refgen import assert_allclose_elementwise, assert_close, quantize_mlx_4bit, rand_vec
+
+pytestmark = pytest.mark.gpu
+
+TD = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+OD = {"f32": vxo.F32, "f16": vxo.F16, "bf16": vxo.BF16}
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def u32(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+# ---------------------------------------------------------------- qmm_4bit
+QMM_REF_CASES = [
+    # (dtype, m, n, k, seed_x, seed_w, seed_bias, atol, rtol)  metal_qmm_4bit_parity.rs
+    ("bf16", 4, 256, 1024, 11, 12, None, 5e-2, 5e-2),
+    ("f16", 2, 128, 512, 21, 22, None, 1e-2, 1e-2),
+    ("f32", 1, 64, 128, 31, 32, None, 1e-4, 1e-4),
+    ("bf16", 2, 128, 512, 41, 42, 43, 5e-2, 5e-2),
+    ("bf16", 8, 3072, 1024, 51, 52, None, 0.5, 0.05),
+]
+
+
+@pytest.mark.parametrize("case", QMM_REF_CASES, ids=lambda c: f"{c[0]}-m{c[1]}n{c[2]}k{c[3]}")
+def test_qmm_reference_cases(cuda, case):
+    dt, m, n, k, sx, sw, sb, atol, rtol = case
+    x = rand_vec(m * k, sx).reshape(m, k)
+    w = rand_vec(n * k, sw)
+    qw, sc, bi = quantize_mlx_4bit(w, n, k, 64)
+    bias = rand_vec(n, sb) if sb is not None else None
+    cpu = vxo.qmm_4bit(x, qw, sc, bi, bias, 64)
+    y = __import__("velox_amd.ops", fromlist=["x"]).qmm_4bit(
+        dev(x, TD[dt]), u32(qw), dev(sc, TD[dt]), dev(bi, TD[dt]),
+        None if bias is None else dev(bias, TD[dt]), 64)
+    assert_close(f"qmm {dt}", host(y), cpu, atol, rtol)
+
+
+def synth_linear(n, k, seed):
+    from velox_amd import synth
+
+    return synth.qlinear(seed, f"cfg1.{n}x{k}", n, k, 64)
+
+
+CFG1_SHAPES = [(4608, 2560), (6144, 2560), (2560, 4096), (9728, 2560), (2560, 9728), (19456, 2560),
+               (151936, 2560)]
+
+
+@pytest.mark.parametrize("m", [5, 80])
+@pytest.mark.parametrize("shape", CFG1_SHAPES, ids=lambda s: f"n{s[0]}k{s[1]}")
+def test_qmm_config1_f16(cuda, m, shape):
+    """Config 1: f16 activations ~N(0,1), seed 1; logits-style tolerance 1e-2 + 1e-2|ref|."""
+    from velox_amd import ops
+
+    n, k = shape
+    lin = synth_linear(n, k, 1)
+    rng = np.random.Generator(np.random.Philox(key=[1, n * 7 + k]))
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    y = ops.qmm_4bit(dev(x), u32(lin["qweight"]), dev(lin["scales"]), dev(lin["biases"]), None, 64)
+    torch.cuda.synchronize()
+    y2 = ops.qmm_4bit(dev(x), u32(lin["qweight"]), dev(lin["scales"]), dev(lin["biases"]), None, 64)
+    assert torch.equal(y, y2), "split-K reduction must be deterministic"
+    cols = np.arange(n) if n <= 20000 else np.sort(np.random.default_rng(0).choice(n, 4096, replace=False))
+    cpu = vxo.qmm_4bit(x.astype(np.float32), lin["qweight"][cols], lin["scales"][cols].astype(np.float32),
+                       lin["biases"][cols].astype(np.float32), None, 64, threads=8)
+    got = host(y)[:, cols]
+    assert_allclose_elementwise(f"cfg1 m{m} {n}x{k}", got, vxo.round_to(cpu, vxo.F16), 1e-2, 1e-2)
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 80, 97])
+def test_qmm_bf16_fast_path_shapes(cuda, m):
+    """bf16 activations (the reference's bf16 contract) through the MFMA path."""
+    from velox_amd import ops
+
+    n, k = 2560, 2560
+    lin = synth_linear(n, k, 5)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    xb = vxo.round_to(x, vxo.BF16)
+    sc = vxo.round_to(lin["scales"].astype(np.float32), vxo.BF16)
+    bi = vxo.round_to(lin["biases"].astype(np.float32), vxo.BF16)
+    y = ops.qmm_4bit(dev(xb, torch.bfloat16), u32(lin["qweight"]), dev(sc, torch.bfloat16),
+                     dev(bi, torch.bfloat16), None, 64)
+    cpu = vxo.qmm_4bit(xb, lin["qweight"], sc, bi, None, 64, threads=8)
+    assert_allclose_elementwise(f"bf16 m{m}", host(y), cpu, 2e-2, 1e-2)
+
+
+def test_qmm_epilogues(cuda):
+    """Residual and SwiGLU epilogues of the fused verify forward (f16 X, bf16 rounding)."""
+    from velox_amd import _lib, ops
+
+    m, k, f = 80, 2560, 1024
+    gate = synth_linear(f, k, 7)
+    up = synth_linear(f, k, 8)
+    x = vxo.round_to(np.random.default_rng(3).standard_normal((m, k)).astype(np.float32), vxo.BF16)
+    # interleave 16-row blocks gate|up as the engine does
+    qw = np.concatenate([np.stack([gate["qweight"][i:i + 16], up["qweight"][i:i + 16]]).reshape(32, -1)
+                         for i in range(0, f, 16)])
+    sc = np.concatenate([np.stack([gate["scales"][i:i + 16], up["scales"][i:i + 16]]).reshape(32, -1)
+                         for i in range(0, f, 16)])
+    bi = np.concatenate([np.stack([gate["biases"][i:i + 16], up["biases"][i:i + 16]]).reshape(32, -1)
+                         for i in range(0, f, 16)])
+    out = torch.zeros((m, f), dtype=torch.float16, device="cuda")
+    ops.qmm_4bit_ex(dev(x, torch.float16), u32(qw), dev(sc), dev(bi), out, epilogue=_lib.EPI_SWIGLU)
+    g = vxo.round_to(vxo.qmm_4bit(x, gate["qweight"], gate["scales"].astype(np.float32),
+                                  gate["biases"].astype(np.float32), None, 64, 8), vxo.BF16)
+    u = vxo.round_to(vxo.qmm_4bit(x, up["qweight"], up["scales"].astype(np.float32),
+                                  up["biases"].astype(np.float32), None, 64, 8), vxo.BF16)
+    silu = vxo.round_to(g / (1 + np.exp(-g.astype(np.float64))).astype(np.float32), vxo.BF16)
+    ref = vxo.round_to(silu * u, vxo.BF16)
+    # g and u each carry the GEMM parity bound (1e-2 absolute) plus one bf16
+    # ulp (their rounding to bf16 can flip); the product propagates it as
+    # |silu(g)| e_u + |u| |silu'(g)| e_g (|silu'| <= 1.1), plus bf16 output
+    # rounding.
+    def ulp(v):
+        return 2.0 ** (np.floor(np.log2(np.abs(v) + 1e-30)) - 7)
+
+    e_g, e_u = 1e-2 + ulp(g), 1e-2 + ulp(u)
+    bound = np.abs(silu) * e_u + 1.1 * np.abs(u) * e_g + 1e-2 * np.abs(ref) + 1e-3
+    d = np.abs(host(out) - ref)
+    assert (d <= bound).all(), f"swiglu: {int((d > bound).sum())} elements beyond the propagated bound"
+    # residual: y = round(R + round(acc))
+    o = synth_linear(1024, k, 9)
+    r = vxo.round_to(np.random.default_rng(4).standard_normal((m, 1024)).astype(np.float32) * 100, vxo.BF16)
+    rt = dev(r, torch.bfloat16)
+    ops.qmm_4bit_ex(dev(x, torch.float16), u32(o["qweight"]), dev(o["scales"]), dev(o["biases"]), rt,
+                    residual=rt, epilogue=_lib.EPI_RESIDUAL)
+    acc = vxo.round_to(vxo.qmm_4bit(x, o["qweight"], o["scales"].astype(np.float32),
+                                    o["biases"].astype(np.float32), None, 64, 8), vxo.BF16)
+    ref = vxo.round_to(r + acc, vxo.BF16)
+    # the GEMM bound (1e-2) plus one bf16 ulp of the rounded GEMM output and of the sum
+    bound = 1e-2 + ulp(acc) + ulp(ref) + 1e-2 * np.abs(ref)
+    d = np.abs(host(rt) - ref)
+    assert (d <= bound).all(), f"residual: {int((d > bound).sum())} elements beyond the propagated bound"
+
+
+def test_qmm_validation_errors(cuda):
+    from velox_amd import ops
+    from velox_amd._lib import VeloxError
+
+    x = torch.zeros((2, 12), dtype=torch.float16, device="cuda")
+    with pytest.raises(VeloxError, match="multiple of 8"):
+        ops.qmm_4bit(x, torch.zeros((4, 1), dtype=torch.int32, device="cuda"),
+                     torch.zeros((4, 1), dtype=torch.float16, device="cuda"),
+                     torch.zeros((4, 1), dtype=torch.float16, device="cuda"), None, 64)
+
+
+# ---------------------------------------------------------------- attention
+DECODE_CASES = [  # metal_decode_parity.rs:150-256
+    ("f32", 1, 4, 2, 32, 4, 4, 2, [5], [0, 1], 42),
+    ("f16", 2, 8, 2, 64, 8, 16, 3, [10, 21], [3, 5, 0, 0, 1, 2], 7),
+    ("bf16", 4, 16, 8, 128, 16, 16, 5, [16, 32, 48, 64],
+     [0, 1, 0, 0, 0, 2, 3, 0, 0, 0, 4, 5, 6, 0, 0, 7, 8, 9, 10, 0], 13),
+    ("bf16", 8, 16, 8, 128, 64, 16, 16, [240] * 8, [((s * 16 + b) % 64) for s in range(8) for b in range(16)], 99),
+    ("bf16", 2, 16, 8, 128, 4, 16, 1, [1, 1], [0, 1], 3),
+]
+DECODE_TOL = {"f32": (1e-4, 1e-4), "f16": (5e-3, 5e-3), "bf16": (3e-2, 3e-2)}
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: f"{c[0]}-n{c[1]}-d{c[4]}")
+def test_decode_attention_reference_cases(cuda, case):
+    from velox_amd import ops
+
+    dt, n, hq, hk, d, p, ps, mb, kv_lens, bt, seed = case
+    scale = 1.0 / np.sqrt(d)
+    q = vxo.round_to(rand_vec(n * hq * d, seed), OD[dt]).reshape(n, hq, d)
+    k = vxo.round_to(rand_vec(p * hk * ps * d, seed + 1), OD[dt]).reshape(p, hk, ps, d)
+    v = vxo.round_to(rand_vec(p * hk * ps * d, seed + 2), OD[dt]).reshape(p, hk, ps, d)
+    bt = np.array(bt, np.uint32).reshape(n, mb)
+    out = ops.paged_decode_attention(dev(q, TD[dt]), dev(k, TD[dt]), dev(v, TD[dt]), u32(bt),
+                                     u32(np.array(kv_lens, np.uint32)), scale)
+    cu = np.arange(n + 1, dtype=np.uint32)
+    kvo = np.array(kv_lens, np.uint32) - 1
+    cpu = vxo.paged_attention(q, k, v, bt, cu, kvo, scale)
+    atol, rtol = DECODE_TOL[dt]
+    assert_close(f"decode {dt}", host(out), cpu, atol, rtol)
+
+
+def _prefill_case(new_lens, kv_offsets, bt, p, seed, dt="bf16", hq=16, hk=8, d=128, ps=16, tree=None):
+    from velox_amd import ops
+
+    cu = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.uint32)
+    total = int(cu[-1])
+    sid = np.repeat(np.arange(len(new_lens)), new_lens).astype(np.uint32)
+    scale = 1.0 / np.sqrt(d)
+    q = vxo.round_to(rand_vec(total * hq * d, seed), OD[dt]).reshape(total, hq, d)
+    k = vxo.round_to(rand_vec(p * hk * ps * d, seed + 1), OD[dt]).reshape(p, hk, ps, d)
+    v = vxo.round_to(rand_vec(p * hk * ps * d, seed + 2), OD[dt]).reshape(p, hk, ps, d)
+    bt = np.asarray(bt, np.uint32).reshape(len(new_lens), -1)
+    kvo = np.asarray(kv_offsets, np.uint32)
+    tm = None
+    if tree is not None:
+        masks, _ = vxo.tree_masks(np.asarray(tree, np.int32))
+        tm = np.tile(masks, len(new_lens))
+    out = ops.paged_prefill_attention(dev(q, TD[dt]), dev(k, TD[dt]), dev(v, TD[dt]), u32(bt), u32(cu), u32(sid),
+                                      u32(kvo), scale,
+                                      tree_mask=None if tm is None else torch.from_numpy(tm.view(np.int64)).cuda())
+    cpu = vxo.paged_attention(q, k, v, bt, cu, kvo, scale, tree_mask=tm)
+    return host(out), cpu
+
+
+def test_prefill_attention_one_seq(cuda):
+    got, ref = _prefill_case([12], [0], [0, 0, 0, 0], 8, 21)  # metal_batched_kernels_parity.rs:246-295
+    assert_close("prefill one seq", got, ref, 3e-2, 3e-2)
+
+
+def test_prefill_attention_mixed_batch(cuda):
+    got, ref = _prefill_case([8, 4, 1], [0, 20, 10], [0, 0, 0, 0, 2, 3, 0, 0, 4, 0, 0, 0], 16, 31)
+    assert_close("prefill mixed batch", got, ref, 3e-2, 3e-2)
+
+
+@pytest.mark.parametrize("ctx", [47, 300, 1100])
+def test_verify_attention_chain_shuffled_pages(cuda, ctx):
+    """Metric shape: 16 sequences x 5 verify rows, GQA 32/8, d=128, f16 KV,
+    shuffled block tables; block-table permutation must not matter."""
+    rng = np.random.default_rng(ctx)
+    B, R, ps = 16, 5, 16
+    nb = (ctx + R + ps - 1) // ps
+    P = B * nb + 3
+    perm = rng.permutation(P)[: B * nb].reshape(B, nb)
+    offs = rng.integers(max(1, ctx - 40), ctx + 1, size=B)
+    got, ref = _prefill_case([R] * B, offs, perm, P, 5, dt="f16", hq=32, hk=8)
+    assert_allclose_elementwise("verify chain", got, ref, 1e-2, 1e-2)
+
+
+def tree_4_2_2():
+    """16 draft nodes (4 + 8 + 4) under the root: node 0 = root, depth-1 nodes
+    1-4, each with 2 children (5-12), and nodes 5 and 6 each with 2 children
+    (13-16)."""
+    par = [-1, 0, 0, 0, 0]
+    for p in range(1, 5):
+        par += [p, p]
+    for p in (5, 6):
+        par += [p, p]
+    return par
+
+
+def test_verify_attention_tree(cuda):
+    par = tree_4_2_2()
+    R, B, ps, ctx = len(par), 4, 16, 200
+    nb = (ctx + R + ps - 1) // ps
+    rng = np.random.default_rng(3)
+    perm = rng.permutation(B * nb).reshape(B, nb)
+    got, ref = _prefill_case([R] * B, [ctx] * B, perm, B * nb, 9, dt="f16", hq=32, hk=8, tree=par)
+    assert_allclose_elementwise("tree attention", got, ref, 1e-2, 1e-2)
+
+
+def test_chain_tree_equals_causal(cuda):
+    chain = [-1, 0, 1, 2, 3]
+    a, _ = _prefill_case([5, 5], [30, 61], [1, 2, 3, 4, 5, 6, 7, 8, 9, 10], 11, 17, dt="f16", tree=chain)
+    b, _ = _prefill_case([5, 5], [30, 61], [1, 2, 3, 4, 5, 6, 7, 8, 9, 10], 11, 17, dt="f16")
+    assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------- rope / scatter
+def test_rope_bf16_reference_case(cuda):
+    from velox_amd import ops
+
+    n, h, d, half, lmax = 4, 16, 128, 64, 1024  # metal_batched_kernels_parity.rs:78-111
+    x = vxo.round_to(rand_vec(n * h * d, 1), vxo.BF16).reshape(n, h, d)
+    c = vxo.round_to(rand_vec(lmax * half, 2), vxo.BF16).reshape(lmax, half)
+    s = vxo.round_to(rand_vec(lmax * half, 3), vxo.BF16).reshape(lmax, half)
+    off = np.array([0, 5, 100, 511], np.uint32)
+    xt = dev(x, torch.bfloat16)
+    ops.batched_rope_decode(xt, dev(c, torch.bfloat16), dev(s, torch.bfloat16), u32(off))
+    cpu = vxo.rope_apply(x, c, s, off, vxo.BF16)
+    assert_close("rope bf16", host(xt), cpu, 5e-2, 5e-2)
+    assert np.array_equal(host(xt), cpu), "same arithmetic, same rounding: bit-identical"
+
+
+def test_rope_f32_reference_case(cuda):
+    from velox_amd import ops
+
+    n, h, d, half, lmax = 2, 4, 64, 32, 256
+    x = rand_vec(n * h * d, 5).reshape(n, h, d)
+    c = rand_vec(lmax * half, 6).reshape(lmax, half)
+    s = rand_vec(lmax * half, 7).reshape(lmax, half)
+    off = np.array([3, 200], np.uint32)
+    xt = dev(x)
+    ops.batched_rope_decode(xt, dev(c), dev(s), u32(off))
+    assert_close("rope f32", host(xt), vxo.rope_apply(x, c, s, off), 1e-5, 1e-5)
+
+
+def test_batched_scatter_byte_exact(cuda):
+    from velox_amd import ops
+
+    p, h, s, d, n = 8, 8, 16, 128, 4  # metal_batched_kernels_parity.rs:144-189
+    pool = vxo.round_to(rand_vec(p * h * s * d, 11), vxo.BF16).reshape(p, h, s, d)
+    val = vxo.round_to(rand_vec(n * h * d, 13), vxo.BF16).reshape(n, h, d)
+    pid = np.array([0, 3, 5, 7], np.uint32)
+    sl = np.array([0, 7, 15, 5], np.uint32)
+    pt = dev(pool, torch.bfloat16)
+    ops.batched_scatter(pt, dev(val, torch.bfloat16), u32(pid), u32(sl))
+    assert np.array_equal(host(pt), vxo.kv_scatter(pool, val, pid, sl))
+
+
+# ---------------------------------------------------------------- acceptance
+def _planted_logits(rng, b, r, v, dtype):
+    lg = rng.normal(0, 3, size=(b, r, v)).astype(np.float32)
+    # plant exact ties at the max (first index must win) in some rows
+    for i in range(0, b * r, 3):
+        row = lg.reshape(-1, v)[i]
+        j1, j2 = sorted(rng.choice(v, 2, replace=False))
+        row[j1] = row[j2] = row.max() + 1.0
+    lg.reshape(-1, v)[5, :] = -np.inf  # all -inf row -> index 0
+    return vxo.round_to(lg, OD[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_accept_greedy_exact(cuda, dtype):
+    from velox_amd import ops
+
+    rng = np.random.default_rng(11)
+    B, k, V = 16, 4, 151936
+    lg = _planted_logits(rng, B, k + 1, V, dtype)
+    am = lg.reshape(-1, V).argmax(axis=1).reshape(B, k + 1)
+    cand = am[:, :k].astype(np.uint32).copy()
+    for b in range(B):  # reject at a random position for half of the sequences
+        if b % 2:
+            cand[b, rng.integers(0, k)] += 1
+    acc, tok = ops.accept_greedy(dev(lg, TD[dtype]), u32(cand))
+    ref_acc, ref_tok = vxo.accept_greedy(lg, cand)
+    assert np.array_equal(acc.cpu().numpy(), ref_acc)
+    for b in range(B):
+        a = ref_acc[b]
+        assert np.array_equal(tok.cpu().numpy().view(np.uint32)[b, : a + 1], ref_tok[b, : a + 1])
+    am_gpu = ops.argmax_rows(dev(lg.reshape(-1, V), TD[dtype])).cpu().numpy().view(np.uint32)
+    assert np.array_equal(am_gpu, np.array([vxo.argmax(r) for r in lg.reshape(-1, V)], np.uint32))
+
+
+@pytest.mark.parametrize("k", [4, 8])
+def test_accept_stochastic_config2_bit_exact(cuda, k):
+    """Config 2: B=16, V=151936, target ~N(0,3), draft = target + N(0,1), T=0.8,
+    Philox(seed 2) uniforms.  Candidates drawn from q, then accept/resample:
+    every token and accepted length must equal the host definition."""
+    from velox_amd import ops
+
+    B, V, T = 16, 151936, 0.8
+    rng = np.random.Generator(np.random.Philox(key=[2, k]))
+    tl = rng.normal(0, 3, size=(B, k + 1, V)).astype(np.float32)
+    dl = (tl[:, :k] + rng.normal(0, 1, size=(B, k, V))).astype(np.float32)
+    uni = vxo.spec_uniforms(2, 0, 0, B, k)
+    inv_t = np.float32(1.0) / np.float32(T)
+    cand = vxo.sample_draft(dl, uni, inv_t)
+    u_draft = np.ascontiguousarray(uni[:, :k, 0]).reshape(-1)
+    cand_gpu = ops.sample_rows(dev(dl.reshape(B * k, V)), dev(u_draft), T).cpu().numpy().view(np.uint32)
+    assert np.array_equal(cand_gpu, cand.reshape(-1)), "draft draws must be bit-identical"
+    acc, tok = ops.accept_stochastic(dev(tl), dev(dl), u32(cand), dev(uni), T)
+    ref_acc, ref_tok = vxo.accept_stochastic(tl, dl, cand, uni, inv_t)
+    assert np.array_equal(acc.cpu().numpy(), ref_acc)
+    tk = tok.cpu().numpy().view(np.uint32)
+    for b in range(B):
+        a = ref_acc[b]
+        assert np.array_equal(tk[b, : a + 1], ref_tok[b, : a + 1]), f"seq {b}"
+
+
+def test_accept_tree_exact(cuda):
+    from velox_amd import ops
+
+    par = tree_4_2_2()
+    R, B, V = len(par), 8, 151936
+    rng = np.random.default_rng(5)
+    lg = vxo.round_to(rng.normal(0, 3, size=(B, R, V)).astype(np.float32), vxo.BF16)
+    am = lg.reshape(-1, V).argmax(axis=1).reshape(B, R)
+    nt = rng.integers(0, V, size=(B, R)).astype(np.uint32)
+    for b in range(B):  # plant accepted paths of various depths
+        cur = 0
+        for _ in range(b % 4):
+            kids = [j for j in range(R) if par[j] == cur]
+            if not kids:
+                break
+            j = kids[rng.integers(0, len(kids))]
+            nt[b, j] = am[b, cur]
+            cur = j
+    acc, path, tok = ops.accept_tree(dev(lg, torch.bfloat16), par, u32(nt))
+    ra, rp, rt = vxo.accept_tree(lg, np.array(par, np.int32), nt)
+    assert np.array_equal(acc.cpu().numpy(), ra)
+    for b in range(B):
+        a = ra[b]
+        assert np.array_equal(path.cpu().numpy()[b, : a + 1], rp[b, : a + 1])
+        assert np.array_equal(tok.cpu().numpy().view(np.uint32)[b, : a + 1], rt[b, : a + 1])

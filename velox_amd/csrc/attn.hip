@@ -1,0 +1,562 @@
+// Paged attention for verify rows (chain or tree) and prefill, gfx950.
+//
+// Replaces paged_prefill_attention / paged_decode_attention (reference
+// src/paged/metal_kernels.rs MSL :107-191, :307-395; hosts :1227-1383,
+// :1680-1846).  The reference walks the KV serially once per (query row,
+// q-head); here one wave handles every query row of a sequence tile times
+// every q-head of a GQA group against one KV head, so each K/V page is read
+// once per (sequence, kv-head, split):
+//   * S^T = K . Q^T on v_mfma_f32_16x16x32_{f16,bf16}: K rows come straight
+//     from the page (16-byte loads along head_dim), Q^T lives in registers;
+//   * online softmax per query column (exp2 with log2e folded into the scale);
+//   * O^T = V^T . P^T: P^T is the S^T accumulator re-packed in registers, V is
+//     transposed through LDS (key-contiguous rows) so each A fragment is two
+//     8-byte LDS reads;
+//   * the KV range is split across workgroups (flash-decoding); a second
+//     kernel merges the partial (m, l, O) of each (sequence, kv-head, tile) in
+//     split order, so results are deterministic and no workgroup waits on
+//     another (a device-scope fence costs an XCD-wide L2 writeback on gfx950).
+// Visibility: causal (kv_len = kv_offset + t + 1, the reference's rule) or a
+// per-row tree mask over the tree slots [kv_offset, kv_offset + 64).
+// f32 tensors use a plain per-(row, head) kernel with the reference's loop.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "vx_common.h"
+
+namespace vx {
+namespace {
+
+constexpr int kKeyBlock = 64;
+constexpr size_t kAttnCounterBytes = 65536;
+
+struct AttnArgs {
+    const void *q;
+    const void *k;
+    const void *v;
+    const uint32_t *bt;
+    const uint32_t *cu;       // mode 0: cu_seqlens [n_seqs+1]
+    const uint32_t *kvo;      // mode 0: kv_offsets; mode 1: kv_lens
+    const uint64_t *tmask;    // [total_q] or null
+    void *out;
+    float *partial;
+    int mode;  // 0: varlen rows (cu_seqlens), 1: decode (row i = seq i)
+    int n_seqs, max_blocks, num_pages, h_q, h_kv, G, D, ps;
+    int qr;      // query rows per tile
+    int n_qtiles, n_splits, chunk;  // keys per split
+    float scale_log2;               // scale * log2(e)
+    uint32_t window;
+    int out_bf16_round;  // round the output to bf16 before the 16-bit store
+};
+
+template <int KT>
+struct MfmaT;
+template <>
+struct MfmaT<VX_F16> {
+    typedef half8_t frag;
+    static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint16_t cvt(float f) { return f32_to_f16_bits(f); }
+};
+template <>
+struct MfmaT<VX_BF16> {
+    typedef bf16x8_t frag;
+    static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint16_t cvt(float f) { return f32_to_bf16_bits(f); }
+};
+
+__device__ __forceinline__ void row_info(const AttnArgs &a, int seq, int &r_seq, int &row0, int &off) {
+    if (a.mode == 0) {
+        row0 = (int)a.cu[seq];
+        r_seq = (int)a.cu[seq + 1] - row0;
+        off = (int)a.kvo[seq];
+    } else {
+        row0 = seq;
+        r_seq = 1;
+        off = (int)a.kvo[seq] - 1;  // kv_len - 1 (kv_len 0 handled by the caller)
+    }
+}
+
+// D: head dim (multiple of 32, <= 256); QT: query tiles of 16 per wave.
+template <int KT, int D, int QT>
+__global__ __launch_bounds__(64) void paged_attn_kernel(AttnArgs a) {
+    typedef typename MfmaT<KT>::frag frag;
+    constexpr int DK = D / 32;  // MFMA k-steps over head_dim
+    constexpr int DT = D / 16;  // output row tiles of O^T
+    constexpr int VT_STRIDE = kKeyBlock + 4;  // halves per transposed V row (bank spread)
+    __shared__ uint16_t vt[D * VT_STRIDE];
+
+    const int lane = threadIdx.x;
+    const int lq = lane & 15;
+    const int lg = lane >> 4;
+    int item = blockIdx.x;
+    const int split = item % a.n_splits;
+    item /= a.n_splits;
+    const int qtile = item % a.n_qtiles;
+    item /= a.n_qtiles;
+    const int hk = item % a.h_kv;
+    const int seq = item / a.h_kv;
+
+    int r_seq, row0, off;
+    row_info(a, seq, r_seq, row0, off);
+    if (a.mode == 1 && (int)a.kvo[seq] == 0) r_seq = 0;  // kv_len 0: zero-filled by the launcher
+    const int t0 = qtile * a.qr;
+    if (t0 >= r_seq) return;  // empty tile: every split of it exits, no merge needed
+    const int t_end = min(r_seq, t0 + a.qr);
+    const int nq = max(0, (t_end - t0)) * a.G;  // live query vectors in this tile
+
+    // key range of this tile: causal upper bound or the tree span
+    const int kv_end = a.tmask ? off + r_seq : off + t_end;
+    const int k_lo = split * a.chunk;
+    const int k_hi = min(kv_end, k_lo + a.chunk);
+
+    // ---- Q^T fragments: query n = 16*qt + lq; row t0 + n / G, head hk*G + n % G
+    frag qf[QT][DK];
+    int q_row[QT];
+    uint64_t q_mask[QT];
+    int q_lim[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+        const int n = qt * 16 + lq;
+        const int t = t0 + n / a.G;
+        const bool live = n < nq;
+        q_row[qt] = live ? row0 + t : -1;
+        q_mask[qt] = (live && a.tmask) ? a.tmask[row0 + t] : 0ull;
+        q_lim[qt] = live ? off + t + 1 : 0;  // causal exclusive bound
+        const int hq = hk * a.G + (n % a.G);
+#pragma unroll
+        for (int ks = 0; ks < DK; ks++) {
+            uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+            if (live)
+                raw = *(const uint4 *)((const uint16_t *)a.q + ((int64_t)(row0 + t) * a.h_q + hq) * D + ks * 32 + lg * 8);
+            qf[qt][ks] = __builtin_bit_cast(frag, raw);
+        }
+    }
+
+    floatx4 o[DT][QT];
+#pragma unroll
+    for (int i = 0; i < DT; i++)
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) o[i][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    float m_run[QT], l_run[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+        m_run[qt] = -__builtin_inff();
+        l_run[qt] = 0.f;
+    }
+
+    const int64_t head_stride = (int64_t)a.ps * D;
+    const int64_t page_stride = (int64_t)a.h_kv * head_stride;
+    const uint32_t *btr = a.bt + (int64_t)seq * a.max_blocks;
+    const int win = (int)a.window;
+
+    for (int kb = k_lo; kb < k_hi; kb += kKeyBlock) {
+        // ---- S^T for 64 keys: 4 tiles of 16 keys
+        floatx4 s[4][QT];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const int key = kb + mt * 16 + lq;
+            const int blk = min(key / a.ps, a.max_blocks - 1);
+            const int page = min((int)btr[blk], a.num_pages - 1);
+            const uint16_t *kr = (const uint16_t *)a.k + page * page_stride + hk * head_stride + (int64_t)(key % a.ps) * D;
+            frag kf[DK];
+#pragma unroll
+            for (int ks = 0; ks < DK; ks++) kf[ks] = __builtin_bit_cast(frag, *(const uint4 *)(kr + ks * 32 + lg * 8));
+#pragma unroll
+            for (int qt = 0; qt < QT; qt++) {
+                floatx4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < DK; ks++) c = MfmaT<KT>::mma(kf[ks], qf[qt][ks], c);
+                s[mt][qt] = c;
+            }
+        }
+        // ---- stage V^T for the block (lane = key): vt[d][key]
+        {
+            const int key = kb + lane;
+            const int blk = min(key / a.ps, a.max_blocks - 1);
+            const int page = min((int)btr[blk], a.num_pages - 1);
+            const uint16_t *vr = (const uint16_t *)a.v + page * page_stride + hk * head_stride + (int64_t)(key % a.ps) * D;
+            __syncthreads();
+#pragma unroll
+            for (int c = 0; c < D / 8; c++) {
+                uint4 raw = *(const uint4 *)(vr + c * 8);
+                const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    vt[(c * 8 + 2 * e) * VT_STRIDE + lane] = (uint16_t)(w4[e] & 0xffffu);
+                    vt[(c * 8 + 2 * e + 1) * VT_STRIDE + lane] = (uint16_t)(w4[e] >> 16);
+                }
+            }
+        }
+        // ---- mask, scale, block max
+        float bmax[QT];
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+            bmax[qt] = -__builtin_inff();
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = kb + mt * 16 + lg * 4 + r;
+                    bool vis = q_row[qt] >= 0 && key < k_hi;
+                    if (vis) {
+                        if (a.tmask) {
+                            if (key >= off) vis = (key - off) < 64 && ((q_mask[qt] >> (key - off)) & 1ull);
+                        } else {
+                            vis = key < q_lim[qt];
+                        }
+                        if (win > 0 && q_lim[qt] > win && key < q_lim[qt] - win) vis = false;
+                    }
+                    const float v = vis ? s[mt][qt][r] * a.scale_log2 : -__builtin_inff();
+                    s[mt][qt][r] = v;
+                    bmax[qt] = fmaxf(bmax[qt], v);
+                }
+            bmax[qt] = fmaxf(bmax[qt], __shfl_xor(bmax[qt], 16));
+            bmax[qt] = fmaxf(bmax[qt], __shfl_xor(bmax[qt], 32));
+        }
+        // ---- probabilities, running stats, rescale O
+        frag pf[QT][2];
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+            const float m_new = fmaxf(m_run[qt], bmax[qt]);
+            const bool dead = m_new == -__builtin_inff();
+            const float alpha = dead ? 1.f : exp2f(m_run[qt] - m_new);
+            float psum = 0.f;
+            uint16_t ph[4][4];
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = dead ? 0.f : exp2f(s[mt][qt][r] - m_new);
+                    psum += p;
+                    ph[mt][r] = MfmaT<KT>::cvt(p);
+                }
+            psum += __shfl_xor(psum, 16);
+            psum += __shfl_xor(psum, 32);
+            l_run[qt] = l_run[qt] * alpha + psum;
+            m_run[qt] = m_new;
+#pragma unroll
+            for (int i = 0; i < DT; i++) o[i][qt] *= alpha;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                unsigned short tmp[8] __attribute__((aligned(16)));
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    tmp[r] = ph[2 * st][r];
+                    tmp[4 + r] = ph[2 * st + 1][r];
+                }
+                pf[qt][st] = *(frag *)tmp;
+            }
+        }
+        __syncthreads();
+        // ---- O^T += V^T . P^T ; A element e <-> key 32*st + 4*lg + (e < 4 ? e : 12 + e)
+#pragma unroll
+        for (int i = 0; i < DT; i++) {
+            const uint16_t *vrow = vt + (i * 16 + lq) * VT_STRIDE;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                uint2 lo = *(const uint2 *)(vrow + st * 32 + lg * 4);
+                uint2 hi = *(const uint2 *)(vrow + st * 32 + 16 + lg * 4);
+                const frag vf = __builtin_bit_cast(frag, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int qt = 0; qt < QT; qt++) o[i][qt] = MfmaT<KT>::mma(vf, pf[qt][st], o[i][qt]);
+            }
+        }
+    }
+
+    // ---- single split: write the output; else publish (m, l, O) for the merge
+    const int64_t tile_id = ((int64_t)seq * a.h_kv + hk) * a.n_qtiles + qtile;
+    if (a.n_splits > 1) {
+        // partial layout per (tile, split): m[64], l[64], O[64][D]
+        float *pbase = a.partial + (tile_id * a.n_splits + split) * (int64_t)(128 + 64 * D);
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+            const int n = qt * 16 + lq;
+            if (lg == 0) {
+                pbase[n] = m_run[qt];
+                pbase[64 + n] = l_run[qt];
+            }
+#pragma unroll
+            for (int i = 0; i < DT; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) pbase[128 + (int64_t)n * D + i * 16 + lg * 4 + r] = o[i][qt][r];
+        }
+        return;
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+        if (q_row[qt] < 0) continue;
+        const int n = qt * 16 + lq;
+        const int hq = hk * a.G + (n % a.G);
+        const float inv = 1.0f / l_run[qt];
+#pragma unroll
+        for (int i = 0; i < DT; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int d = i * 16 + lg * 4 + r;
+                const int64_t oi = ((int64_t)q_row[qt] * a.h_q + hq) * D + d;
+                float val = o[i][qt][r] * inv;
+                if (a.out_bf16_round) val = round_to<VX_BF16>(val);
+                ((uint16_t *)a.out)[oi] = MfmaT<KT>::cvt(val);
+            }
+    }
+}
+
+// Merge the split partials of one (sequence, kv-head, tile) in split order.
+template <int KT>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    int item = blockIdx.x;
+    const int qtile = item % a.n_qtiles;
+    item /= a.n_qtiles;
+    const int hk = item % a.h_kv;
+    const int seq = item / a.h_kv;
+    int r_seq, row0, off;
+    row_info(a, seq, r_seq, row0, off);
+    if (a.mode == 1 && (int)a.kvo[seq] == 0) r_seq = 0;
+    const int t0 = qtile * a.qr;
+    if (t0 >= r_seq) return;
+    const int nq = (min(r_seq, t0 + a.qr) - t0) * a.G;
+    const int64_t tile_id = ((int64_t)seq * a.h_kv + hk) * a.n_qtiles + qtile;
+    const int64_t stride = 128 + 64 * (int64_t)a.D;
+    const float *p0 = a.partial + tile_id * a.n_splits * stride;
+    for (int e = threadIdx.x; e < nq * a.D; e += blockDim.x) {
+        const int n = e / a.D;
+        const int d = e - n * a.D;
+        float M = -__builtin_inff();
+        for (int sp = 0; sp < a.n_splits; sp++) M = fmaxf(M, p0[sp * stride + n]);
+        float L = 0.f, acc = 0.f;
+        for (int sp = 0; sp < a.n_splits; sp++) {
+            const float *ps = p0 + sp * stride;
+            const float ms = ps[n];
+            const float f = ms == -__builtin_inff() ? 0.f : exp2f(ms - M);
+            L += ps[64 + n] * f;
+            acc += ps[128 + (int64_t)n * a.D + d] * f;
+        }
+        float val = acc / L;
+        if (a.out_bf16_round) val = round_to<VX_BF16>(val);
+        const int t = t0 + n / a.G;
+        const int hq = hk * a.G + (n % a.G);
+        ((uint16_t *)a.out)[((int64_t)(row0 + t) * a.h_q + hq) * a.D + d] = MfmaT<KT>::cvt(val);
+    }
+}
+
+// Plain per-(row, q-head) kernel, the reference's loop (MSL :307-395 / :107-191)
+// with a fixed-order tree reduction of q.k; used for f32 tensors.
+template <int DT>
+__global__ void paged_attn_ref_kernel(AttnArgs a, int64_t total_q) {
+    extern __shared__ float sh[];
+    float *qs = sh;
+    float *red = sh + a.D;
+    const int row = blockIdx.x;
+    const int hq = blockIdx.y;
+    const int tid = threadIdx.x;
+    int seq = 0;
+    if (a.mode == 0) {
+        int lo = 0, hi = a.n_seqs - 1;
+        while (lo < hi) {  // last seq with cu[seq] <= row
+            const int mid = (lo + hi + 1) / 2;
+            if ((int)a.cu[mid] <= row) lo = mid; else hi = mid - 1;
+        }
+        seq = lo;
+    } else {
+        seq = row;
+    }
+    int r_seq, row0, off;
+    row_info(a, seq, r_seq, row0, off);
+    const int t = row - row0;
+    const int hk = hq / a.G;
+    int end = a.tmask ? off + r_seq : off + t + 1;
+    if (a.mode == 1) end = (int)a.kvo[seq];
+    const int self_len = off + t + 1;
+    const int start = (a.window > 0 && self_len > (int)a.window) ? self_len - (int)a.window : 0;
+    if (tid < a.D) qs[tid] = ld_elem<DT>(a.q, ((int64_t)row * a.h_q + hq) * a.D + tid);
+    __syncthreads();
+    float acc = 0.f, m = -__builtin_inff(), l = 0.f;
+    const uint64_t tm = a.tmask ? a.tmask[row] : 0ull;
+    for (int pos = start; pos < end; pos++) {
+        if (a.tmask && pos >= off) {
+            const int j = pos - off;
+            if (j >= 64 || !((tm >> j) & 1ull)) continue;
+        }
+        const int page = min((int)a.bt[(int64_t)seq * a.max_blocks + min(pos / a.ps, a.max_blocks - 1)], a.num_pages - 1);
+        const int64_t base = (((int64_t)page * a.h_kv + hk) * a.ps + pos % a.ps) * a.D;
+        red[tid] = tid < a.D ? qs[tid] * ld_elem<DT>(a.k, base + tid) : 0.f;
+        __syncthreads();
+        for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
+            if (tid < stride) red[tid] += red[tid + stride];
+            __syncthreads();
+        }
+        const float s = red[0] * (a.scale_log2 * 0.69314718055994531f);
+        __syncthreads();
+        const float new_m = fmaxf(m, s);
+        const float alpha = __expf(m - new_m);
+        const float beta = __expf(s - new_m);
+        if (tid < a.D) acc = acc * alpha + beta * ld_elem<DT>(a.v, base + tid);
+        l = l * alpha + beta;
+        m = new_m;
+    }
+    if (tid < a.D) st_elem<DT>(a.out, ((int64_t)row * a.h_q + hq) * a.D + tid, l > 0.f ? acc / l : 0.f);
+}
+
+__global__ void zero_u16_kernel(uint16_t *p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+template <int KT, int D, int QT>
+void launch_attn(const AttnArgs &a, int64_t n_items, hipStream_t st) {
+    hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT>), dim3((unsigned)n_items), dim3(64), 0, st, a);
+}
+
+template <int KT>
+int dispatch_attn(const AttnArgs &a, int QT, int64_t n_items, hipStream_t st) {
+#define VX_ACASE(d, qt)                                       \
+    if (a.D == d && QT == qt) {                              \
+        launch_attn<KT, d, qt>(a, n_items, st);              \
+        return 0;                                            \
+    }
+    VX_ACASE(32, 1) VX_ACASE(32, 2) VX_ACASE(32, 4)
+    VX_ACASE(64, 1) VX_ACASE(64, 2) VX_ACASE(64, 4)
+    VX_ACASE(128, 1) VX_ACASE(128, 2) VX_ACASE(128, 4)
+    VX_ACASE(256, 1) VX_ACASE(256, 2)
+#undef VX_ACASE
+    return set_error("paged_attention: no kernel for head_dim");
+}
+
+}  // namespace
+
+size_t attn_workspace_bytes(int64_t n_seqs, int64_t h_kv, int64_t n_qtiles, int64_t n_splits, int64_t D) {
+    if (n_splits <= 1) return kAttnCounterBytes;
+    return kAttnCounterBytes + (size_t)n_seqs * h_kv * n_qtiles * n_splits * (128 + 64 * D) * 4;
+}
+
+// Shared launcher for the C ABI and the engine.
+int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool, const uint32_t *bt,
+                           const uint32_t *cu, const uint32_t *kvo, const uint64_t *tmask, void *out,
+                           int mode, int64_t total_q, int64_t n_seqs, int64_t max_rows,
+                           int64_t max_blocks, int64_t num_pages, int64_t h_q, int64_t h_kv,
+                           int64_t D, int64_t ps, float scale, uint32_t window, int dtype,
+                           void *workspace, size_t ws_bytes, int64_t max_kv, hipStream_t st,
+                           int out_bf16_round) {
+    AttnArgs a{};
+    a.out_bf16_round = out_bf16_round;
+    a.q = q;
+    a.k = k_pool;
+    a.v = v_pool;
+    a.bt = bt;
+    a.cu = cu;
+    a.kvo = kvo;
+    a.tmask = tmask;
+    a.out = out;
+    a.mode = mode;
+    a.n_seqs = (int)n_seqs;
+    a.max_blocks = (int)max_blocks;
+    a.num_pages = (int)num_pages;
+    a.h_q = (int)h_q;
+    a.h_kv = (int)h_kv;
+    a.G = (int)(h_q / h_kv);
+    a.D = (int)D;
+    a.ps = (int)ps;
+    a.scale_log2 = scale * 1.44269504088896341f;
+    a.window = window;
+    if (total_q == 0 || n_seqs == 0) return 0;
+    if (dtype == VX_F32) {
+        const int threads = 256;
+        hipLaunchKernelGGL(paged_attn_ref_kernel<VX_F32>, dim3((unsigned)total_q, (unsigned)h_q), dim3(threads),
+                           (size_t)(D + threads) * 4, st, a, total_q);
+        VX_HIP(hipGetLastError());
+        return 0;
+    }
+    const int qn_max = D <= 128 ? 64 : 32;
+    int64_t qn = std::min<int64_t>(max_rows * a.G, qn_max);
+    int QT = (int)std::max<int64_t>(1, vx_cdiv(qn, 16));
+    if (QT == 3) QT = 4;
+    a.qr = std::max(1, (QT * 16) / a.G);
+    a.n_qtiles = (int)vx_cdiv(max_rows, a.qr);
+    // KV split: aim for ~2 waves per SIMD across the chip
+    const int64_t base_items = n_seqs * h_kv * a.n_qtiles;
+    const int64_t max_keys = std::max<int64_t>(1, max_kv);
+    const int64_t target = 4LL * device_cu_count() * 2;
+    int64_t splits = std::max<int64_t>(1, target / std::max<int64_t>(1, base_items));
+    int64_t chunk = vx_cdiv(vx_cdiv(max_keys, splits), kKeyBlock) * kKeyBlock;
+    chunk = std::max<int64_t>(chunk, 4 * kKeyBlock);
+    splits = vx_cdiv(max_keys, chunk);
+    a.chunk = (int)chunk;
+    a.n_splits = (int)splits;
+    void *ws = workspace;
+    const size_t need = attn_workspace_bytes(n_seqs, h_kv, a.n_qtiles, splits, D);
+    if (splits > 1) {
+        if (!ws) {
+            VX_TRY(stream_workspace(st, need, &ws));
+        } else if (ws_bytes < need) {
+            return set_error("paged_attention: workspace too small");
+        }
+    }
+    a.partial = ws ? (float *)((char *)ws + kAttnCounterBytes) : nullptr;
+    if (mode == 1) {
+        // decode rows with kv_len == 0 keep zeros (metal_kernels.rs:2395-2397)
+        const int64_t tot = total_q * h_q * D;
+        hipLaunchKernelGGL(zero_u16_kernel, dim3((unsigned)vx_cdiv(tot, 256)), dim3(256), 0, st, (uint16_t *)out, tot);
+    }
+    const int64_t n_items = base_items * splits;
+    int rc = dtype == VX_F16 ? dispatch_attn<VX_F16>(a, QT, n_items, st) : dispatch_attn<VX_BF16>(a, QT, n_items, st);
+    if (rc) return rc;
+    if (splits > 1) {
+        if (dtype == VX_F16)
+            hipLaunchKernelGGL(attn_combine_kernel<VX_F16>, dim3((unsigned)base_items), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL(attn_combine_kernel<VX_BF16>, dim3((unsigned)base_items), dim3(256), 0, st, a);
+    }
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace vx
+
+using namespace vx;
+
+static int check_attn_shapes(int64_t h_q, int64_t h_kv, int64_t D, int dtype) {
+    VX_REQUIRE(h_kv > 0 && h_q % h_kv == 0, "paged_attention: H_q must be divisible by H_kv");
+    VX_REQUIRE(D <= 256, "paged_attention: head_dim > D_MAX 256");
+    VX_REQUIRE(D % 32 == 0, "paged_attention: head_dim must be a multiple of 32");
+    VX_REQUIRE(dtype == VX_F32 || dtype == VX_F16 || dtype == VX_BF16, "paged_attention: unsupported dtype");
+    return 0;
+}
+
+extern "C" int vx_paged_attention(const void *q, const void *k_pool, const void *v_pool,
+                                  const uint32_t *block_table, const uint32_t *cu_seqlens,
+                                  const uint32_t *seq_id_per_q, const uint32_t *kv_offsets,
+                                  const uint64_t *tree_mask, void *out, int64_t total_q,
+                                  int64_t n_seqs, int64_t max_blocks, int64_t num_pages,
+                                  int64_t h_q, int64_t h_kv, int64_t head_dim, int64_t page_size,
+                                  float scale, uint32_t sliding_window, int dtype, void *stream) {
+    VX_TRY(check_attn_shapes(h_q, h_kv, head_dim, dtype));
+    VX_REQUIRE(q && k_pool && v_pool && block_table && cu_seqlens && kv_offsets && out,
+               "paged_attention: null tensor");
+    VX_REQUIRE(max_blocks > 0 && num_pages > 0 && page_size > 0, "paged_attention: empty pool");
+    (void)seq_id_per_q;  // rows are located through cu_seqlens
+    // rows per sequence and KV length are bounded by total_q and the block table
+    return paged_attention_launch(q, k_pool, v_pool, block_table, cu_seqlens, kv_offsets, tree_mask,
+                                  out, 0, total_q, n_seqs, total_q, max_blocks, num_pages, h_q, h_kv,
+                                  head_dim, page_size, scale, sliding_window, dtype, nullptr, 0,
+                                  max_blocks * page_size, (hipStream_t)stream, 0);
+}
+
+extern "C" int vx_paged_decode_attention(const void *q, const void *k_pool, const void *v_pool,
+                                         const uint32_t *block_table, const uint32_t *kv_lens,
+                                         void *out, int64_t n, int64_t max_blocks, int64_t num_pages,
+                                         int64_t h_q, int64_t h_kv, int64_t head_dim,
+                                         int64_t page_size, float scale, uint32_t sliding_window,
+                                         int dtype, void *stream) {
+    VX_TRY(check_attn_shapes(h_q, h_kv, head_dim, dtype));
+    VX_REQUIRE(q && k_pool && v_pool && block_table && kv_lens && out, "paged_decode_attention: null tensor");
+    VX_REQUIRE(max_blocks > 0 && num_pages > 0 && page_size > 0, "paged_decode_attention: empty pool");
+    return paged_attention_launch(q, k_pool, v_pool, block_table, nullptr, kv_lens, nullptr, out, 1, n, n,
+                                  1, max_blocks, num_pages, h_q, h_kv, head_dim, page_size, scale,
+                                  sliding_window, dtype, nullptr, 0, max_blocks * page_size,
+                                  (hipStream_t)stream, 0);
+}

@@ -1,0 +1,1180 @@
+// Engine level of the verify path: PagedKvCache (reference src/paged/pages.rs),
+// PagedQwen3 forward / forward_all (src/paged/qwen3.rs:943-1037) and
+// SpecEngine prefill / step / free (src/paged/spec.rs), hosted in C++ over the
+// gfx950 kernels.
+//
+// Numerics follow the reference's bf16 model (vb.dtype() == BF16, as in
+// tests/spec_decode.rs:162): every tensor value is rounded to bf16 at the same
+// points as candle's ops.  GEMM inputs, Q and the KV pages are stored as f16,
+// which holds each of those bf16 values exactly (|v| < 65504), so the MFMA
+// f16 path computes on the reference's values.  The MLP product uses a 2^-8
+// storage scale (exact) to keep |v| < 65504 in f16.
+//
+// One round (spec.rs:186-316) on the device:
+//   host: grow block tables (all-or-nothing page allocation), build every
+//         forward's row metadata and upload it in one copy;
+//   D draft forwards over the batch (argmax -> next draft input on device);
+//   one verify forward over batch x (D+1) rows; one acceptance launch;
+//   one device->host copy of (accepted, committed tokens, candidates).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "vx_common.h"
+
+namespace vx {
+
+// ---------------------------------------------------------------------------
+// library state
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+int set_error(const std::string &msg) {
+    g_err = msg;
+    return -1;
+}
+int hip_error(hipError_t e, const char *what) {
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    return -2;
+}
+
+int device_cu_count() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+    cache[dev] = cus;
+    return cus;
+}
+
+int stream_workspace(hipStream_t s, size_t bytes, void **out) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> ws;
+    int dev = 0;
+    VX_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(mu);
+    auto &e = ws[{dev, s}];
+    if (e.first && e.second >= bytes) {
+        *out = e.first;
+        return 0;
+    }
+    size_t sz = std::max(bytes, e.second * 2);
+    sz = (sz + 4095) & ~(size_t)4095;
+    if (e.first) {
+        VX_HIP(hipStreamSynchronize(s));
+        VX_HIP(hipFree(e.first));
+        e.first = nullptr;
+        e.second = 0;
+    }
+    void *p = nullptr;
+    VX_HIP(hipMalloc(&p, sz));
+    VX_HIP(hipMemsetAsync(p, 0, sz, s));
+    e.first = p;
+    e.second = sz;
+    *out = p;
+    return 0;
+}
+
+// kernels in the other translation units
+int qmm_fast(const void *x, const uint32_t *w, const void *s, const void *b, void *y, const void *resid,
+             int64_t M, int64_t N, int64_t K, int x_dt, int x_shift, int round_dt, int y_dt, int epi,
+             void *workspace, size_t ws_bytes, hipStream_t st);
+int qmm_fast_scaled(const void *x, const uint32_t *w, const void *s, const void *b, void *y,
+                    const void *resid, int64_t M, int64_t N, int64_t K, int x_shift, int y_shift,
+                    int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes, hipStream_t st);
+size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi);
+size_t attn_workspace_bytes(int64_t n_seqs, int64_t h_kv, int64_t n_qtiles, int64_t n_splits, int64_t D);
+int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool, const uint32_t *bt,
+                           const uint32_t *cu, const uint32_t *kvo, const uint64_t *tmask, void *out,
+                           int mode, int64_t total_q, int64_t n_seqs, int64_t max_rows,
+                           int64_t max_blocks, int64_t num_pages, int64_t h_q, int64_t h_kv,
+                           int64_t D, int64_t ps, float scale, uint32_t window, int dtype,
+                           void *workspace, size_t ws_bytes, int64_t max_kv, hipStream_t st,
+                           int out_bf16_round);
+size_t accept_workspace_bytes(int64_t rows, int64_t vocab);
+size_t stochastic_workspace_bytes(int64_t rows, int64_t vocab);
+int argmax_accept_launch(const void *logits, int ldt, int64_t rows, int64_t vocab, int mode,
+                         int rows_per_group, const uint32_t *cand, int k, int32_t *accepted,
+                         uint32_t *tokens, int32_t *path, const int32_t *parents, uint32_t *argmax_out,
+                         uint32_t *next_ids, int64_t next_stride, void *ws, size_t ws_bytes,
+                         hipStream_t st);
+int sample_rows_launch(const void *logits, int ldt, const float *uni, int64_t ustride, uint32_t *out,
+                       int64_t rows, int64_t vocab, float temperature, uint32_t *next_ids,
+                       int64_t next_stride, void *ws, size_t ws_bytes, hipStream_t st);
+int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint32_t *cand,
+                             const float *uni, int32_t *accepted, uint32_t *tokens, int64_t batch,
+                             int64_t k, int64_t vocab, float temperature, void *ws, size_t ws_bytes,
+                             hipStream_t st);
+int embed_launch(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_t rows, int64_t H,
+                 int64_t vocab, hipStream_t st);
+int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
+                   int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
+int qk_rope_scatter_launch(const uint16_t *qkv, const uint16_t *qn, const uint16_t *kn,
+                           const uint16_t *cos_t, const uint16_t *sin_t, const uint32_t *pos,
+                           const uint32_t *pages, const uint32_t *slots, uint16_t *qout,
+                           uint16_t *kp, uint16_t *vp, int64_t rows, int HQ, int HK, int D, int ps,
+                           float eps, int kv_dt, hipStream_t st);
+
+// ---------------------------------------------------------------------------
+// host-side 16-bit conversions (RNE), identical to the device converts
+// ---------------------------------------------------------------------------
+static inline float h2f(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            float v = (float)m * (1.0f / 16777216.0f);
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+static inline uint16_t f2bf(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+}
+static inline float bf2f(uint16_t h) {
+    uint32_t x = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+static inline uint16_t f2h(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+    if (ax < 0x33000000u) return (uint16_t)sign;
+    const int e = (int)(ax >> 23) - 127;
+    const uint32_t mant = (ax & 0x7fffffu) | 0x800000u;
+    if (e >= -14) {
+        uint32_t h = ((uint32_t)(e + 15) << 10) | ((mant >> 13) & 0x3ffu);
+        const uint32_t rem = mant & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    const int s = -e - 1;
+    uint32_t h = mant >> s;
+    const uint32_t rem = mant & ((1u << s) - 1u), half = 1u << (s - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+// f16 -> bf16 value (candle VarBuilder to_dtype), kept in an f16 carrier
+static inline uint16_t f16_as_bf16_carrier(uint16_t h) { return f2h(bf2f(f2bf(h2f(h)))); }
+static inline uint16_t f16_to_bf16_bits(uint16_t h) { return f2bf(h2f(h)); }
+
+}  // namespace vx
+
+using namespace vx;
+
+// ===========================================================================
+// pages (pages.rs)
+// ===========================================================================
+struct vx_pages {
+    int64_t layers = 0, kv_heads = 0, head_dim = 0, page_size = 0, num_pages = 0;
+    int dtype = VX_F16;
+    int device = 0;
+    void *base = nullptr;
+    size_t pool_bytes = 0;  // per (layer, K|V)
+    std::vector<uint32_t> free_list;
+    std::vector<uint32_t> refcount;
+    std::mutex mu;
+};
+
+extern "C" int vx_pages_create(int64_t layers, int64_t kv_heads, int64_t head_dim, int64_t page_size,
+                               int64_t num_pages, int kv_dtype, vx_pages **out) {
+    VX_REQUIRE(out, "pages: null out");
+    VX_REQUIRE(layers > 0 && num_pages > 0, "PagedKvCache must have >=1 layer and >=1 page");
+    VX_REQUIRE(num_pages <= (int64_t)UINT32_MAX, "num_pages exceeds u32 range");
+    VX_REQUIRE(kv_dtype == VX_F16 || kv_dtype == VX_BF16, "pages: kv dtype must be f16 or bf16");
+    auto p = std::make_unique<vx_pages>();
+    p->layers = layers;
+    p->kv_heads = kv_heads;
+    p->head_dim = head_dim;
+    p->page_size = page_size;
+    p->num_pages = num_pages;
+    p->dtype = kv_dtype;
+    VX_HIP(hipGetDevice(&p->device));
+    p->pool_bytes = (size_t)num_pages * kv_heads * page_size * head_dim * 2;
+    const size_t total = p->pool_bytes * layers * 2;
+    VX_HIP(hipMalloc(&p->base, total));
+    VX_HIP(hipMemset(p->base, 0, total));
+    p->free_list.resize(num_pages);
+    for (int64_t i = 0; i < num_pages; i++) p->free_list[i] = (uint32_t)(num_pages - 1 - i);
+    p->refcount.assign(num_pages, 0);
+    *out = p.release();
+    return 0;
+}
+
+extern "C" void vx_pages_destroy(vx_pages *p) {
+    if (!p) return;
+    if (p->base) (void)hipFree(p->base);
+    delete p;
+}
+
+extern "C" int vx_pages_alloc(vx_pages *p, int64_t n, uint32_t *out_pages) {
+    VX_REQUIRE(p && (out_pages || n == 0), "pages: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    if ((int64_t)p->free_list.size() < n) return set_error("alloc: not enough free pages");
+    for (int64_t i = 0; i < n; i++) {
+        const uint32_t pg = p->free_list.back();
+        p->free_list.pop_back();
+        p->refcount[pg] = 1;
+        out_pages[i] = pg;
+    }
+    return 0;
+}
+
+extern "C" void vx_pages_incref(vx_pages *p, const uint32_t *pages, int64_t n) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(p->mu);
+    for (int64_t i = 0; i < n; i++)
+        if ((int64_t)pages[i] < p->num_pages && p->refcount[pages[i]] >= 1) p->refcount[pages[i]]++;
+}
+
+extern "C" void vx_pages_free(vx_pages *p, const uint32_t *pages, int64_t n) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(p->mu);
+    for (int64_t i = 0; i < n; i++) {
+        const uint32_t pg = pages[i];
+        if ((int64_t)pg >= p->num_pages || p->refcount[pg] == 0) continue;
+        if (--p->refcount[pg] == 0) p->free_list.push_back(pg);
+    }
+}
+
+extern "C" int64_t vx_pages_num_free(const vx_pages *p) {
+    if (!p) return 0;
+    std::lock_guard<std::mutex> lk(const_cast<vx_pages *>(p)->mu);
+    return (int64_t)p->free_list.size();
+}
+
+extern "C" uint32_t vx_pages_refcount(const vx_pages *p, uint32_t page) {
+    if (!p || (int64_t)page >= p->num_pages) return 0;
+    std::lock_guard<std::mutex> lk(const_cast<vx_pages *>(p)->mu);
+    return p->refcount[page];
+}
+
+extern "C" void *vx_pages_pool(vx_pages *p, int64_t layer, int kv) {
+    if (!p || layer < 0 || layer >= p->layers) return nullptr;
+    return (char *)p->base + (size_t)(layer * 2 + (kv ? 1 : 0)) * p->pool_bytes;
+}
+
+// ===========================================================================
+// model (qwen3.rs)
+// ===========================================================================
+namespace {
+
+struct QLinDev {
+    uint32_t *w = nullptr;
+    uint16_t *s = nullptr, *b = nullptr;  // f16 carriers of the bf16 affine params
+    int64_t n = 0, k = 0;
+};
+
+struct LayerDev {
+    uint16_t *ln1, *ln2, *qn, *kn;  // bf16
+    QLinDev qkv, o, gu, down;
+};
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t n = 0;
+    int ensure(size_t bytes) {
+        if (n >= bytes) return 0;
+        if (p) VX_HIP(hipFree(p));
+        p = nullptr;
+        n = 0;
+        VX_HIP(hipMalloc(&p, bytes));
+        n = bytes;
+        return 0;
+    }
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+// Row metadata of one forward, built on the host and uploaded as one blob.
+struct Meta {
+    int64_t rows = 0, n_seqs = 0, max_blocks = 1, max_rows = 1, max_kv = 1;
+    bool tree = false;
+    // offsets (bytes) inside the blob
+    size_t o_pos, o_page, o_slot, o_cu, o_kvo, o_bt, o_mask, o_last, size;
+};
+
+constexpr int kMlpShift = 8;  // MLP product stored as v * 2^-8 in f16
+
+// Opt-in per-kernel timing with HIP events recorded on the launch stream.
+enum ProfClass { PC_QMM = 0, PC_ATTN = 1, PC_OTHER = 2, PC_N = 3 };
+struct Prof {
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    size_t used = 0;
+    struct Rec {
+        hipEvent_t a, b;
+        int cls;
+        double bytes;
+    };
+    std::vector<Rec> recs;
+    hipEvent_t next() {
+        if (used == pool.size()) {
+            hipEvent_t e;
+            (void)hipEventCreate(&e);
+            pool.push_back(e);
+        }
+        return pool[used++];
+    }
+    void reset() {
+        used = 0;
+        recs.clear();
+    }
+    ~Prof() {
+        for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+    }
+};
+
+struct ProfScope {
+    Prof *p;
+    hipStream_t st;
+    Prof::Rec r{};
+    ProfScope(Prof *p_, hipStream_t st_, int cls, double bytes) : p(p_), st(st_) {
+        if (!p || !p->on) return;
+        r.a = p->next();
+        r.b = p->next();
+        r.cls = cls;
+        r.bytes = bytes;
+        (void)hipEventRecord(r.a, st);
+    }
+    ~ProfScope() {
+        if (!p || !p->on) return;
+        (void)hipEventRecord(r.b, st);
+        p->recs.push_back(r);
+    }
+};
+
+// algorithmic bytes of one int4 GEMM launch: packed weights + f16 affine
+// params (0.5625 B/weight), X read once, Y written once (+ R read)
+double qmm_bytes(int64_t M, int64_t N, int64_t K, bool resid) {
+    return 0.5625 * (double)N * K + 2.0 * M * K + 2.0 * M * N * (resid ? 2 : 1);
+}
+
+}  // namespace
+
+struct vx_model {
+    vx_qwen3_config cfg{};
+    int64_t L = 0;
+    int device = 0;
+    uint16_t *embed = nullptr;  // bf16 [V, H]
+    std::vector<LayerDev> layers;
+    uint16_t *norm = nullptr;
+    QLinDev lm;
+    uint16_t *cos_t = nullptr, *sin_t = nullptr;  // bf16 [max_pos, D/2]
+    std::vector<void *> allocs;
+    // activations
+    DevBuf h, xn, qkv, q, attn, act, ids, meta, ws;
+    int64_t cap_rows = 0;
+    ~vx_model() {
+        for (void *p : allocs) (void)hipFree(p);
+    }
+};
+
+namespace {
+
+int dev_upload(vx_model *m, const void *src, size_t bytes, void **dst) {
+    void *p = nullptr;
+    VX_HIP(hipMalloc(&p, std::max<size_t>(bytes, 16)));
+    m->allocs.push_back(p);
+    VX_HIP(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice));
+    *dst = p;
+    return 0;
+}
+
+// Concatenate linears row-wise (optionally interleaving 16-row blocks of two
+// linears) and convert the affine params to bf16 values in f16 carriers.
+int upload_qlin(vx_model *m, const std::vector<const vx_qlinear_host *> &parts,
+                const std::vector<int64_t> &ns, int64_t k, bool interleave16, QLinDev *out) {
+    const int64_t g = k / 64, kw = k / 8;
+    int64_t n = 0;
+    for (int64_t x : ns) n += x;
+    std::vector<uint32_t> w((size_t)(n * kw));
+    std::vector<uint16_t> s((size_t)(n * g)), b((size_t)(n * g));
+    auto put_row = [&](int64_t dst, const vx_qlinear_host *src, int64_t r) {
+        memcpy(&w[dst * kw], src->qweight + r * kw, kw * 4);
+        for (int64_t j = 0; j < g; j++) {
+            s[dst * g + j] = f16_as_bf16_carrier(src->scales[r * g + j]);
+            b[dst * g + j] = f16_as_bf16_carrier(src->biases[r * g + j]);
+        }
+    };
+    if (interleave16) {
+        const int64_t f = ns[0];
+        if (ns.size() != 2 || ns[1] != f || f % 16) return set_error("gate/up interleave needs equal N % 16 == 0");
+        for (int64_t blk = 0; blk < f / 16; blk++)
+            for (int64_t i = 0; i < 16; i++) {
+                put_row(blk * 32 + i, parts[0], blk * 16 + i);
+                put_row(blk * 32 + 16 + i, parts[1], blk * 16 + i);
+            }
+    } else {
+        int64_t row = 0;
+        for (size_t p = 0; p < parts.size(); p++)
+            for (int64_t r = 0; r < ns[p]; r++) put_row(row++, parts[p], r);
+    }
+    out->n = n;
+    out->k = k;
+    VX_TRY(dev_upload(m, w.data(), w.size() * 4, (void **)&out->w));
+    VX_TRY(dev_upload(m, s.data(), s.size() * 2, (void **)&out->s));
+    VX_TRY(dev_upload(m, b.data(), b.size() * 2, (void **)&out->b));
+    return 0;
+}
+
+int upload_bf16(vx_model *m, const uint16_t *f16, int64_t n, uint16_t **out) {
+    std::vector<uint16_t> t((size_t)n);
+    for (int64_t i = 0; i < n; i++) t[i] = f16_to_bf16_bits(f16[i]);
+    return dev_upload(m, t.data(), t.size() * 2, (void **)out);
+}
+
+}  // namespace
+
+extern "C" int vx_model_create(const vx_qwen3_config *cfg, const vx_weights_host *w, int64_t n_layers,
+                               vx_model **out) {
+    VX_REQUIRE(cfg && w && out, "model: null argument");
+    const int64_t L = n_layers > 0 ? std::min(n_layers, cfg->layers) : cfg->layers;
+    const int64_t H = cfg->hidden, F = cfg->inter, D = cfg->head_dim, HQ = cfg->n_heads, HK = cfg->n_kv_heads;
+    VX_REQUIRE(cfg->group_size == 64, "model: only MLX int4 group_size 64 is supported");
+    VX_REQUIRE(H % 256 == 0 && F % 256 == 0 && (HQ * D) % 256 == 0, "model: hidden/inter/heads*head_dim must be multiples of 256");
+    VX_REQUIRE(HK > 0 && HQ % HK == 0, "model: n_heads must be divisible by n_kv_heads");
+    VX_REQUIRE(D % 32 == 0 && D <= 256, "model: head_dim must be a multiple of 32 and <= 256");
+    VX_REQUIRE(F % 16 == 0, "model: intermediate size must be a multiple of 16");
+    auto m = std::make_unique<vx_model>();
+    m->cfg = *cfg;
+    m->L = L;
+    VX_HIP(hipGetDevice(&m->device));
+    VX_TRY(upload_bf16(m.get(), w->embed, cfg->vocab * H, &m->embed));
+    VX_TRY(upload_bf16(m.get(), w->norm, H, &m->norm));
+    {
+        std::vector<const vx_qlinear_host *> p = {&w->lm_head};
+        VX_TRY(upload_qlin(m.get(), p, {cfg->vocab}, H, false, &m->lm));
+    }
+    m->layers.resize(L);
+    for (int64_t i = 0; i < L; i++) {
+        const vx_layer_host &lh = w->layers[i];
+        LayerDev &ld = m->layers[i];
+        VX_TRY(upload_bf16(m.get(), lh.ln1, H, &ld.ln1));
+        VX_TRY(upload_bf16(m.get(), lh.ln2, H, &ld.ln2));
+        VX_TRY(upload_bf16(m.get(), lh.q_norm, D, &ld.qn));
+        VX_TRY(upload_bf16(m.get(), lh.k_norm, D, &ld.kn));
+        VX_TRY(upload_qlin(m.get(), {&lh.q, &lh.k, &lh.v}, {HQ * D, HK * D, HK * D}, H, false, &ld.qkv));
+        VX_TRY(upload_qlin(m.get(), {&lh.o}, {H}, HQ * D, false, &ld.o));
+        VX_TRY(upload_qlin(m.get(), {&lh.gate, &lh.up}, {F, F}, H, true, &ld.gu));
+        VX_TRY(upload_qlin(m.get(), {&lh.down}, {H}, F, false, &ld.down));
+    }
+    // RoPE tables (qwen3.rs:278-295): f64 inv_freq -> f32, t * inv_freq in f32,
+    // sin/cos in f32, then the model dtype.
+    const int64_t half = D / 2;
+    std::vector<float> inv(half);
+    for (int64_t j = 0; j < half; j++) inv[j] = 1.0f / (float)std::pow(cfg->rope_theta, (double)(2 * j) / (double)D);
+    std::vector<uint16_t> ct((size_t)(cfg->max_pos * half)), stt((size_t)(cfg->max_pos * half));
+    for (int64_t t = 0; t < cfg->max_pos; t++)
+        for (int64_t j = 0; j < half; j++) {
+            const float f = (float)t * inv[j];
+            ct[t * half + j] = f2bf(cosf(f));
+            stt[t * half + j] = f2bf(sinf(f));
+        }
+    VX_TRY(dev_upload(m.get(), ct.data(), ct.size() * 2, (void **)&m->cos_t));
+    VX_TRY(dev_upload(m.get(), stt.data(), stt.size() * 2, (void **)&m->sin_t));
+    *out = m.release();
+    return 0;
+}
+
+extern "C" void vx_model_destroy(vx_model *m) { delete m; }
+
+namespace {
+
+struct SeqDesc {
+    int64_t new_tokens, kv_offset;
+    const uint32_t *bt;
+    int64_t n_blocks;
+};
+
+// Build the metadata blob for one forward (host side).  Fails like the
+// reference when a block table is too short (qwen3.rs:682-689).
+int build_meta(const vx_model *m, const vx_pages *pg, const SeqDesc *seqs, int64_t n, const int32_t *parents,
+               std::vector<uint8_t> &blob, Meta &meta) {
+    meta = Meta{};
+    meta.n_seqs = n;
+    int64_t rows = 0;
+    for (int64_t s = 0; s < n; s++) {
+        rows += seqs[s].new_tokens;
+        meta.max_blocks = std::max(meta.max_blocks, seqs[s].n_blocks);
+        meta.max_rows = std::max(meta.max_rows, seqs[s].new_tokens);
+        meta.max_kv = std::max(meta.max_kv, seqs[s].kv_offset + seqs[s].new_tokens);
+        if (parents && seqs[s].new_tokens != seqs[0].new_tokens)
+            return set_error("forward: tree verify needs equal node counts");
+    }
+    meta.rows = rows;
+    meta.tree = parents != nullptr;
+    const int64_t R = n ? seqs[0].new_tokens : 0;
+    if (parents && R > 64) return set_error("forward: tree larger than 64 nodes");
+    uint64_t tmask[64] = {0};
+    int32_t depth[64] = {0};
+    if (parents)
+        for (int64_t i = 0; i < R; i++) {
+            uint64_t mk = 1ull << i;
+            int32_t d = 0;
+            for (int32_t p = parents[i]; p >= 0; p = parents[p]) {
+                mk |= 1ull << p;
+                d++;
+            }
+            tmask[i] = mk;
+            depth[i] = d;
+        }
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    size_t o = 0;
+    meta.o_pos = o;
+    o = al(o + rows * 4);
+    meta.o_page = o;
+    o = al(o + rows * 4);
+    meta.o_slot = o;
+    o = al(o + rows * 4);
+    meta.o_cu = o;
+    o = al(o + (n + 1) * 4);
+    meta.o_kvo = o;
+    o = al(o + n * 4);
+    meta.o_bt = o;
+    o = al(o + n * meta.max_blocks * 4);
+    meta.o_mask = o;
+    o = al(o + (parents ? rows * 8 : 8));
+    meta.o_last = o;
+    o = al(o + n * 4);
+    meta.size = o;
+    blob.assign(o, 0);
+    uint32_t *pos = (uint32_t *)&blob[meta.o_pos];
+    uint32_t *page = (uint32_t *)&blob[meta.o_page];
+    uint32_t *slot = (uint32_t *)&blob[meta.o_slot];
+    uint32_t *cu = (uint32_t *)&blob[meta.o_cu];
+    uint32_t *kvo = (uint32_t *)&blob[meta.o_kvo];
+    uint32_t *bt = (uint32_t *)&blob[meta.o_bt];
+    uint64_t *mask = (uint64_t *)&blob[meta.o_mask];
+    uint32_t *last = (uint32_t *)&blob[meta.o_last];
+    const int64_t ps = pg->page_size;
+    int64_t row = 0;
+    cu[0] = 0;
+    for (int64_t s = 0; s < n; s++) {
+        const SeqDesc &sd = seqs[s];
+        for (int64_t b = 0; b < sd.n_blocks; b++) {
+            if ((int64_t)sd.bt[b] >= pg->num_pages) return set_error("forward: block table holds an invalid page id");
+            bt[s * meta.max_blocks + b] = sd.bt[b];
+        }
+        for (int64_t t = 0; t < sd.new_tokens; t++, row++) {
+            const int64_t p = sd.kv_offset + t;
+            const int64_t blk = p / ps;
+            if (blk >= sd.n_blocks) return set_error("fused prefill: block_table too short");
+            page[row] = sd.bt[blk];
+            slot[row] = (uint32_t)(p % ps);
+            const int64_t rp = sd.kv_offset + (parents ? depth[t] : t);
+            if (rp >= m->cfg.max_pos) return set_error("forward: position exceeds max_position_embeddings");
+            pos[row] = (uint32_t)rp;
+            if (parents) mask[row] = tmask[t];
+        }
+        cu[s + 1] = (uint32_t)row;
+        kvo[s] = (uint32_t)sd.kv_offset;
+        last[s] = (uint32_t)(row - 1);
+    }
+    return 0;
+}
+
+int ensure_buffers(vx_model *m, int64_t rows) {
+    if (rows <= m->cap_rows) return 0;
+    const vx_qwen3_config &c = m->cfg;
+    const int64_t H = c.hidden, F = c.inter, QW = c.n_heads * c.head_dim, KW = c.n_kv_heads * c.head_dim;
+    const int64_t R = std::max<int64_t>(rows, 16);
+    VX_TRY(m->h.ensure(R * H * 2));
+    VX_TRY(m->xn.ensure(R * std::max({H, QW, F}) * 2));
+    VX_TRY(m->qkv.ensure(R * (QW + 2 * KW) * 2));
+    VX_TRY(m->q.ensure(R * QW * 2));
+    VX_TRY(m->attn.ensure(R * QW * 2));
+    VX_TRY(m->act.ensure(R * F * 2));
+    VX_TRY(m->ids.ensure(R * 4));
+    m->cap_rows = R;
+    return 0;
+}
+
+size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int64_t n_seqs, int64_t max_rows,
+                        int64_t max_kv) {
+    const vx_qwen3_config &c = m->cfg;
+    const int64_t H = c.hidden, F = c.inter, QW = c.n_heads * c.head_dim, KW = c.n_kv_heads * c.head_dim;
+    size_t need = 0;
+    need = std::max(need, qmm_workspace_bytes(rows, QW + 2 * KW, H, VX_EPI_STORE));
+    need = std::max(need, qmm_workspace_bytes(rows, H, QW, VX_EPI_RESIDUAL));
+    need = std::max(need, qmm_workspace_bytes(rows, 2 * F, H, VX_EPI_SWIGLU));
+    need = std::max(need, qmm_workspace_bytes(rows, H, F, VX_EPI_RESIDUAL));
+    need = std::max(need, qmm_workspace_bytes(logit_rows, c.vocab, H, VX_EPI_STORE));
+    // attention: upper bound on its split plan (see paged_attention_launch)
+    const int64_t G = c.n_heads / c.n_kv_heads;
+    const int64_t qn_max = c.head_dim <= 128 ? 64 : 32;
+    int64_t qt = std::max<int64_t>(1, vx_cdiv(std::min<int64_t>(max_rows * G, qn_max), 16));
+    if (qt == 3) qt = 4;
+    const int64_t qr = std::max<int64_t>(1, qt * 16 / G);
+    const int64_t nqt = vx_cdiv(max_rows, qr);
+    const int64_t splits = std::max<int64_t>(1, vx_cdiv(max_kv, 128));
+    need = std::max(need, attn_workspace_bytes(n_seqs, c.n_kv_heads, nqt, splits, c.head_dim));
+    return need;
+}
+
+// Forward over `rows` rows whose token ids are already on the device.
+int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &meta, const uint8_t *meta_dev,
+                int all_rows, void *logits, void *ws, size_t ws_bytes, hipStream_t st, Prof *prof = nullptr,
+                double kv_bytes_per_layer = 0.0) {
+    const vx_qwen3_config &c = m->cfg;
+    const int64_t H = c.hidden, F = c.inter, D = c.head_dim, HQ = c.n_heads, HK = c.n_kv_heads;
+    const int64_t QW = HQ * D, KW = HK * D, R = meta.rows;
+    const float eps = (float)c.rms_eps;
+    VX_REQUIRE(pg->kv_heads == HK && pg->head_dim == D, "forward: pages do not match the model");
+    VX_REQUIRE(pg->layers >= m->L, "forward: pages have fewer layers than the model");
+    VX_REQUIRE(pg->dtype == VX_F16, "forward: the fused verify path keeps KV pages in f16");
+    const uint32_t *pos = (const uint32_t *)(meta_dev + meta.o_pos);
+    const uint32_t *pages = (const uint32_t *)(meta_dev + meta.o_page);
+    const uint32_t *slots = (const uint32_t *)(meta_dev + meta.o_slot);
+    const uint32_t *cu = (const uint32_t *)(meta_dev + meta.o_cu);
+    const uint32_t *kvo = (const uint32_t *)(meta_dev + meta.o_kvo);
+    const uint32_t *bt = (const uint32_t *)(meta_dev + meta.o_bt);
+    const uint64_t *mask = meta.tree ? (const uint64_t *)(meta_dev + meta.o_mask) : nullptr;
+    const uint32_t *last = (const uint32_t *)(meta_dev + meta.o_last);
+    uint16_t *h = (uint16_t *)m->h.p, *xn = (uint16_t *)m->xn.p, *qkv = (uint16_t *)m->qkv.p;
+    uint16_t *q = (uint16_t *)m->q.p, *attn = (uint16_t *)m->attn.p, *act = (uint16_t *)m->act.p;
+    const float scale = 1.0f / sqrtf((float)D);
+
+    {
+        ProfScope ps_(prof, st, PC_OTHER, 0.0);
+        VX_TRY(embed_launch(ids_dev, m->embed, h, R, H, c.vocab, st));
+    }
+    for (int64_t l = 0; l < m->L; l++) {
+        const LayerDev &ly = m->layers[l];
+        uint16_t *kp = (uint16_t *)vx_pages_pool(pg, l, 0);
+        uint16_t *vp = (uint16_t *)vx_pages_pool(pg, l, 1);
+        {
+            ProfScope ps_(prof, st, PC_OTHER, 0.0);
+            VX_TRY(rmsnorm_launch(h, ly.ln1, xn, nullptr, R, H, eps, VX_F16, st));
+        }
+        {
+            ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, QW + 2 * KW, H, false));
+            VX_TRY(qmm_fast_scaled(xn, ly.qkv.w, ly.qkv.s, ly.qkv.b, qkv, nullptr, R, QW + 2 * KW, H, 0, 0, VX_BF16,
+                                   VX_BF16, VX_EPI_STORE, ws, ws_bytes, st));
+        }
+        {
+            ProfScope ps_(prof, st, PC_OTHER, 0.0);
+            VX_TRY(qk_rope_scatter_launch(qkv, ly.qn, ly.kn, m->cos_t, m->sin_t, pos, pages, slots, q, kp, vp, R,
+                                          (int)HQ, (int)HK, (int)D, (int)pg->page_size, eps, VX_F16, st));
+        }
+        {
+            ProfScope ps_(prof, st, PC_ATTN, kv_bytes_per_layer + 4.0 * R * QW);
+            VX_TRY(paged_attention_launch(q, kp, vp, bt, cu, kvo, mask, attn, 0, R, meta.n_seqs, meta.max_rows,
+                                          meta.max_blocks, pg->num_pages, HQ, HK, D, pg->page_size, scale, 0,
+                                          VX_F16, ws, ws_bytes, meta.max_kv, st, 1));
+        }
+        {
+            ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, H, QW, true));
+            VX_TRY(qmm_fast_scaled(attn, ly.o.w, ly.o.s, ly.o.b, h, h, R, H, QW, 0, 0, VX_BF16, VX_BF16,
+                                   VX_EPI_RESIDUAL, ws, ws_bytes, st));
+        }
+        {
+            ProfScope ps_(prof, st, PC_OTHER, 0.0);
+            VX_TRY(rmsnorm_launch(h, ly.ln2, xn, nullptr, R, H, eps, VX_F16, st));
+        }
+        {
+            ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, 2 * F, H, false) - 2.0 * R * F);
+            VX_TRY(qmm_fast_scaled(xn, ly.gu.w, ly.gu.s, ly.gu.b, act, nullptr, R, 2 * F, H, 0, kMlpShift, VX_BF16,
+                                   VX_F16, VX_EPI_SWIGLU, ws, ws_bytes, st));
+        }
+        {
+            ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, H, F, true));
+            VX_TRY(qmm_fast_scaled(act, ly.down.w, ly.down.s, ly.down.b, h, h, R, H, F, kMlpShift, 0, VX_BF16,
+                                   VX_BF16, VX_EPI_RESIDUAL, ws, ws_bytes, st));
+        }
+    }
+    const int64_t lrows = all_rows ? R : meta.n_seqs;
+    {
+        ProfScope ps_(prof, st, PC_OTHER, 0.0);
+        VX_TRY(rmsnorm_launch(h, m->norm, xn, all_rows ? nullptr : last, lrows, H, eps, VX_F16, st));
+    }
+    {
+        ProfScope ps_(prof, st, PC_QMM, qmm_bytes(lrows, c.vocab, H, false));
+        VX_TRY(qmm_fast_scaled(xn, m->lm.w, m->lm.s, m->lm.b, logits, nullptr, lrows, c.vocab, H, 0, 0, VX_BF16,
+                               VX_BF16, VX_EPI_STORE, ws, ws_bytes, st));
+    }
+    return 0;
+}
+
+int prepare_ws(vx_model *m, const Meta &meta, int all_rows) {
+    const size_t need = forward_ws_bytes(m, meta.rows, all_rows ? meta.rows : meta.n_seqs, meta.n_seqs,
+                                         meta.max_rows, meta.max_kv);
+    if (m->ws.n < need) {
+        VX_HIP(hipDeviceSynchronize());
+        VX_TRY(m->ws.ensure(need));
+        VX_HIP(hipMemset(m->ws.p, 0, m->ws.n));
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int vx_forward(vx_model *m, vx_pages *pages, const uint32_t *input_ids, const vx_seq_slice *seqs,
+                          int64_t n_seqs, int all_rows, const int32_t *tree_parents, void *logits,
+                          void *stream) {
+    VX_REQUIRE(m && pages && input_ids && seqs && logits, "forward: null argument");
+    hipStream_t st = (hipStream_t)stream;
+    std::vector<SeqDesc> sd(n_seqs);
+    for (int64_t i = 0; i < n_seqs; i++) sd[i] = {seqs[i].new_tokens, seqs[i].kv_offset, seqs[i].block_table, seqs[i].n_blocks};
+    std::vector<uint8_t> blob;
+    Meta meta;
+    VX_TRY(build_meta(m, pages, sd.data(), n_seqs, tree_parents, blob, meta));
+    if (meta.rows == 0) return 0;
+    for (int64_t i = 0; i < meta.rows; i++)
+        VX_REQUIRE(input_ids[i] < (uint32_t)m->cfg.vocab, "forward: token id out of range");
+    VX_TRY(ensure_buffers(m, meta.rows));
+    VX_TRY(m->meta.ensure(meta.size));
+    VX_TRY(prepare_ws(m, meta, all_rows));
+    VX_HIP(hipMemcpyAsync(m->meta.p, blob.data(), meta.size, hipMemcpyHostToDevice, st));
+    VX_HIP(hipMemcpyAsync(m->ids.p, input_ids, meta.rows * 4, hipMemcpyHostToDevice, st));
+    VX_TRY(forward_dev(m, pages, (const uint32_t *)m->ids.p, meta, (const uint8_t *)m->meta.p, all_rows, logits,
+                       m->ws.p, m->ws.n, st));
+    // the host blob must outlive the async copy
+    VX_HIP(hipStreamSynchronize(st));
+    return 0;
+}
+
+// ===========================================================================
+// spec engine (spec.rs)
+// ===========================================================================
+namespace {
+struct SpecState {
+    std::vector<uint32_t> target_blocks, draft_blocks;
+    int64_t kv_len = 0;
+    uint32_t last_token = 0;
+    std::vector<uint32_t> tokens;
+    uint32_t stream_id = 0, round = 0;
+    bool live = false;
+};
+}  // namespace
+
+struct vx_spec {
+    vx_model *target, *draft;
+    vx_pages *tp, *dp;
+    float temperature;
+    uint64_t seed;
+    int fix_hole;
+    std::vector<SpecState> states;
+    // device buffers for a round
+    DevBuf d_ids, d_cand, d_vids, d_tlog, d_dlog, d_acc, d_tok, d_uni, d_meta, d_argws, d_draw;
+    // host staging (pinned)
+    void *h_stage = nullptr;
+    size_t h_stage_n = 0;
+    std::vector<uint32_t> last_cand;
+    std::vector<float> last_logits;
+    int64_t last_n = 0, last_k = 0;
+    Prof prof_draft, prof_verify;
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    bool profiling = false;
+    vx_step_profile last_prof{};
+    ~vx_spec() {
+        if (h_stage) (void)hipHostFree(h_stage);
+        for (hipEvent_t x : ev)
+            if (x) (void)hipEventDestroy(x);
+    }
+};
+
+extern "C" int vx_spec_create(vx_model *target, vx_pages *target_pages, vx_model *draft, vx_pages *draft_pages,
+                              float temperature, uint64_t sample_seed, int fix_draft_hole, vx_spec **out) {
+    VX_REQUIRE(target && target_pages && draft && draft_pages && out, "spec: null argument");
+    if (target->cfg.vocab != draft->cfg.vocab)
+        return set_error("draft vocab_size (" + std::to_string(draft->cfg.vocab) + ") != target vocab_size (" +
+                         std::to_string(target->cfg.vocab) + "); spec decoding requires matched tokenizers");
+    auto e = std::make_unique<vx_spec>();
+    e->target = target;
+    e->draft = draft;
+    e->tp = target_pages;
+    e->dp = draft_pages;
+    e->temperature = temperature;
+    e->seed = sample_seed;
+    e->fix_hole = fix_draft_hole;
+    *out = e.release();
+    return 0;
+}
+
+extern "C" void vx_spec_destroy(vx_spec *e) { delete e; }
+extern "C" void vx_spec_free(vx_spec *e, int64_t s);
+
+namespace {
+int page_size_or_err(const vx_spec *e, int64_t *ps) {
+    if (e->dp->page_size != e->tp->page_size)
+        return set_error("draft page_size (" + std::to_string(e->dp->page_size) + ") != target page_size (" +
+                         std::to_string(e->tp->page_size) + ")");
+    *ps = e->tp->page_size;
+    return 0;
+}
+
+int ensure_capacity(vx_pages *p, std::vector<uint32_t> &bt, int64_t needed, const char *ctx) {
+    if ((int64_t)bt.size() >= needed) return 0;
+    std::vector<uint32_t> extra(needed - bt.size());
+    if (vx_pages_alloc(p, (int64_t)extra.size(), extra.data()) != 0)
+        return set_error(std::string(ctx) + ": alloc extra pages");
+    bt.insert(bt.end(), extra.begin(), extra.end());
+    return 0;
+}
+
+int stage(vx_spec *e, size_t bytes) {
+    if (e->h_stage_n >= bytes) return 0;
+    if (e->h_stage) VX_HIP(hipHostFree(e->h_stage));
+    e->h_stage = nullptr;
+    VX_HIP(hipHostMalloc(&e->h_stage, bytes, hipHostMallocDefault));
+    e->h_stage_n = bytes;
+    return 0;
+}
+}  // namespace
+
+extern "C" int vx_spec_prefill(vx_spec *e, const uint32_t *const *prompts, const int64_t *lens, int64_t n,
+                               int64_t *out_first_state) {
+    VX_REQUIRE(e && prompts && lens && out_first_state, "prefill: null argument");
+    int64_t ps;
+    VX_TRY(page_size_or_err(e, &ps));
+    for (int64_t b = 0; b < n; b++)
+        VX_REQUIRE(lens[b] >= 2, "speculative prefill requires a prompt with at least 2 tokens");
+    const int64_t first = (int64_t)e->states.size();
+    std::vector<SeqDesc> ts(n), ds(n);
+    std::vector<uint32_t> ids;
+    auto rollback = [&]() {
+        while ((int64_t)e->states.size() > first) {
+            vx_spec_free(e, (int64_t)e->states.size() - 1);
+            e->states.pop_back();
+        }
+        return -1;
+    };
+    for (int64_t b = 0; b < n; b++) {
+        SpecState s;
+        const int64_t head = lens[b] - 1;
+        const int64_t need = (head + 1 + ps - 1) / ps;
+        s.stream_id = (uint32_t)(first + b);
+        if (ensure_capacity(e->tp, s.target_blocks, need, "alloc target prefill pages")) return rollback();
+        if (ensure_capacity(e->dp, s.draft_blocks, need, "alloc draft prefill pages")) {
+            vx_pages_free(e->tp, s.target_blocks.data(), (int64_t)s.target_blocks.size());
+            return rollback();
+        }
+        s.kv_len = head;
+        s.last_token = prompts[b][head];
+        s.tokens.assign(prompts[b], prompts[b] + lens[b]);
+        s.live = true;
+        e->states.push_back(std::move(s));
+        ids.insert(ids.end(), prompts[b], prompts[b] + head);
+    }
+    for (int64_t b = 0; b < n; b++) {
+        SpecState &s = e->states[first + b];
+        ts[b] = {lens[b] - 1, 0, s.target_blocks.data(), (int64_t)s.target_blocks.size()};
+        ds[b] = {lens[b] - 1, 0, s.draft_blocks.data(), (int64_t)s.draft_blocks.size()};
+    }
+    // prefill both models on prompt[..len-1]; logits discarded (spec.rs:172-173)
+    DevBuf lg;
+    VX_TRY(lg.ensure((size_t)n * e->target->cfg.vocab * 2));
+    std::vector<vx_seq_slice> sl(n);
+    for (int64_t b = 0; b < n; b++) sl[b] = {ts[b].new_tokens, 0, ts[b].bt, ts[b].n_blocks};
+    if (vx_forward(e->target, e->tp, ids.data(), sl.data(), n, 0, nullptr, lg.p, nullptr)) return rollback();
+    for (int64_t b = 0; b < n; b++) sl[b] = {ds[b].new_tokens, 0, ds[b].bt, ds[b].n_blocks};
+    if (vx_forward(e->draft, e->dp, ids.data(), sl.data(), n, 0, nullptr, lg.p, nullptr)) return rollback();
+    *out_first_state = first;
+    return 0;
+}
+
+namespace {
+__global__ void build_verify_ids(const uint32_t *last, const uint32_t *cand, uint32_t *vids, int64_t n, int64_t k) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * (k + 1)) return;
+    const int64_t b = i / (k + 1), j = i % (k + 1);
+    vids[i] = j == 0 ? last[b] : cand[b * k + j - 1];
+}
+__global__ void spec_uniforms_kernel(float *out, const uint32_t *streams, const uint32_t *rounds, int64_t n,
+                                     int64_t k, uint32_t k0, uint32_t k1) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * (k + 1)) return;
+    const int64_t b = i / (k + 1), j = i % (k + 1);
+    uint32_t c[4] = {streams[b], rounds[b], (uint32_t)j, 0u};
+    vx_philox(c, k0, k1);
+    for (int t = 0; t < 4; t++) out[i * 4 + t] = vx_u01(c[t]);
+}
+}  // namespace
+
+extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int64_t draft_k, int64_t eos,
+                            vx_round_outcome *outcomes, uint32_t *committed, void *stream) {
+    VX_REQUIRE(e && state_ids && outcomes && committed, "step: null argument");
+    if (draft_k == 0) return set_error("draft_k must be >= 1");
+    VX_REQUIRE(draft_k > 0 && draft_k + 1 <= 64, "step: draft_k out of range");
+    int64_t ps;
+    VX_TRY(page_size_or_err(e, &ps));
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t D = draft_k, V = e->target->cfg.vocab;
+    std::vector<SpecState *> S(n);
+    for (int64_t b = 0; b < n; b++) {
+        VX_REQUIRE(state_ids[b] >= 0 && state_ids[b] < (int64_t)e->states.size() && e->states[state_ids[b]].live,
+                   "step: unknown state");
+        S[b] = &e->states[state_ids[b]];
+    }
+    // capacity (spec.rs:198-205)
+    for (int64_t b = 0; b < n; b++) {
+        VX_TRY(ensure_capacity(e->tp, S[b]->target_blocks, (S[b]->kv_len + D + 1 + ps - 1) / ps, "grow target block table"));
+        VX_TRY(ensure_capacity(e->dp, S[b]->draft_blocks, (S[b]->kv_len + D + ps - 1) / ps, "grow draft block table"));
+    }
+    // metadata for D draft forwards + 1 verify forward
+    std::vector<std::vector<uint8_t>> blobs(D + 1);
+    std::vector<Meta> metas(D + 1);
+    std::vector<SeqDesc> sd(n);
+    for (int64_t i = 0; i < D; i++) {
+        for (int64_t b = 0; b < n; b++)
+            sd[b] = {1, S[b]->kv_len + i, S[b]->draft_blocks.data(), (int64_t)S[b]->draft_blocks.size()};
+        VX_TRY(build_meta(e->draft, e->dp, sd.data(), n, nullptr, blobs[i], metas[i]));
+    }
+    for (int64_t b = 0; b < n; b++)
+        sd[b] = {D + 1, S[b]->kv_len, S[b]->target_blocks.data(), (int64_t)S[b]->target_blocks.size()};
+    VX_TRY(build_meta(e->target, e->tp, sd.data(), n, nullptr, blobs[D], metas[D]));
+    std::vector<size_t> boff(D + 1);
+    size_t total = 0;
+    for (int64_t i = 0; i <= D; i++) {
+        boff[i] = total;
+        total += (metas[i].size + 255) & ~(size_t)255;
+    }
+    const size_t small = (size_t)n * 4 * 3;  // last tokens, stream ids, rounds
+    const size_t res_bytes = (size_t)n * 4 + (size_t)n * (D + 1) * 4 + (size_t)n * D * 4;
+    VX_TRY(stage(e, total + small + res_bytes + 256));
+    uint8_t *hs = (uint8_t *)e->h_stage;
+    for (int64_t i = 0; i <= D; i++) memcpy(hs + boff[i], blobs[i].data(), metas[i].size);
+    uint32_t *h_last = (uint32_t *)(hs + total);
+    uint32_t *h_strm = h_last + n;
+    uint32_t *h_rnd = h_strm + n;
+    for (int64_t b = 0; b < n; b++) {
+        h_last[b] = S[b]->last_token;
+        h_strm[b] = S[b]->stream_id;
+        h_rnd[b] = S[b]->round;
+    }
+    // device buffers
+    VX_TRY(ensure_buffers(e->draft, n));
+    VX_TRY(ensure_buffers(e->target, n * (D + 1)));
+    VX_TRY(e->d_meta.ensure(total + small));
+    VX_TRY(e->d_ids.ensure(n * 4));
+    VX_TRY(e->d_cand.ensure(n * D * 4));
+    VX_TRY(e->d_vids.ensure(n * (D + 1) * 4));
+    VX_TRY(e->d_tlog.ensure((size_t)n * (D + 1) * V * 2));
+    const bool stoch = e->temperature > 0.f;
+    VX_TRY(e->d_dlog.ensure((size_t)n * (stoch ? D : 1) * V * 2));
+    VX_TRY(e->d_acc.ensure(n * 4));
+    VX_TRY(e->d_tok.ensure(n * (D + 1) * 4));
+    VX_TRY(e->d_uni.ensure(n * (D + 1) * 16));
+    VX_TRY(e->d_draw.ensure(n * 4));
+    size_t accws = std::max(accept_workspace_bytes(n * (D + 1), V), stochastic_workspace_bytes(n * (2 * D + 1), V));
+    if (e->d_argws.n < accws) {
+        VX_HIP(hipDeviceSynchronize());
+        VX_TRY(e->d_argws.ensure(accws));
+        VX_HIP(hipMemset(e->d_argws.p, 0, e->d_argws.n));
+    }
+    VX_TRY(prepare_ws(e->draft, metas[0], 0));
+    VX_TRY(prepare_ws(e->target, metas[D], 1));
+    uint8_t *dm = (uint8_t *)e->d_meta.p;
+    VX_HIP(hipMemcpyAsync(dm, hs, total + small, hipMemcpyHostToDevice, st));
+    const uint32_t *d_last = (const uint32_t *)(dm + total);
+    uint32_t *cand = (uint32_t *)e->d_cand.p;
+    uint32_t *ids = (uint32_t *)e->d_ids.p;
+    VX_HIP(hipMemcpyAsync(ids, d_last, n * 4, hipMemcpyDeviceToDevice, st));
+    float *uni = (float *)e->d_uni.p;
+    if (stoch) {
+        hipLaunchKernelGGL(spec_uniforms_kernel, dim3((unsigned)vx_cdiv(n * (D + 1), 256)), dim3(256), 0, st, uni,
+                           d_last + n, d_last + 2 * n, n, D, (uint32_t)e->seed, (uint32_t)(e->seed >> 32));
+        VX_HIP(hipGetLastError());
+    }
+    const bool prof = e->profiling;
+    if (prof) {
+        for (int j = 0; j < 4; j++)
+            if (!e->ev[j]) VX_HIP(hipEventCreate(&e->ev[j]));
+        e->prof_draft.reset();
+        e->prof_verify.reset();
+        e->prof_draft.on = e->prof_verify.on = true;
+        VX_HIP(hipEventRecord(e->ev[0], st));
+    }
+    // KV bytes read per verify layer (K and V of every visible position)
+    double kv_verify = 0.0, kv_draft = 0.0;
+    for (int64_t b = 0; b < n; b++) {
+        kv_verify += (double)(S[b]->kv_len + D + 1) * e->tp->kv_heads * e->tp->head_dim * 2 * 2;
+        kv_draft += (double)(S[b]->kv_len + (D + 1) / 2.0) * e->dp->kv_heads * e->dp->head_dim * 2 * 2;
+    }
+    // ---- draft phase: feed [last, c0 .. c_{D-2}] (spec.rs:223-240)
+    for (int64_t i = 0; i < D; i++) {
+        void *dl = stoch ? (void *)((uint16_t *)e->d_dlog.p + (size_t)i * n * V) : e->d_dlog.p;
+        VX_TRY(forward_dev(e->draft, e->dp, ids, metas[i], dm + boff[i], 0, dl, e->draft->ws.p, e->draft->ws.n, st,
+                           prof ? &e->prof_draft : nullptr, kv_draft));
+        if (!stoch) {
+            VX_TRY(argmax_accept_launch(dl, VX_BF16, n, V, 0, 1, nullptr, 0, nullptr, nullptr, nullptr, nullptr,
+                                        nullptr, cand + i, D, e->d_argws.p, e->d_argws.n, st));
+        } else {
+            VX_TRY(sample_rows_launch(dl, VX_BF16, uni + i * 4, (D + 1) * 4, (uint32_t *)e->d_draw.p, n, V,
+                                      e->temperature, cand + i, D, e->d_argws.p, e->d_argws.n, st));
+        }
+        if (i + 1 < D)  // next draft input = column i of cand [n, D]
+            VX_HIP(hipMemcpy2DAsync(ids, 4, cand + i, D * 4, 4, n, hipMemcpyDeviceToDevice, st));
+    }
+    // ---- verify (spec.rs:246-264)
+    hipLaunchKernelGGL(build_verify_ids, dim3((unsigned)vx_cdiv(n * (D + 1), 256)), dim3(256), 0, st, d_last, cand,
+                       (uint32_t *)e->d_vids.p, n, D);
+    VX_HIP(hipGetLastError());
+    if (prof) VX_HIP(hipEventRecord(e->ev[1], st));
+    VX_TRY(forward_dev(e->target, e->tp, (const uint32_t *)e->d_vids.p, metas[D], dm + boff[D], 1, e->d_tlog.p,
+                       e->target->ws.p, e->target->ws.n, st, prof ? &e->prof_verify : nullptr, kv_verify));
+    if (prof) VX_HIP(hipEventRecord(e->ev[2], st));
+    // ---- acceptance (spec.rs:266-292)
+    if (!stoch) {
+        VX_TRY(argmax_accept_launch(e->d_tlog.p, VX_BF16, n * (D + 1), V, 1, (int)(D + 1), cand, (int)D,
+                                    (int32_t *)e->d_acc.p, (uint32_t *)e->d_tok.p, nullptr, nullptr, nullptr, nullptr,
+                                    0, e->d_argws.p, e->d_argws.n, st));
+    } else {
+        // draft logits are laid out [D][n][V]; the acceptance expects [n][D][V]
+        DevBuf tmp;
+        VX_TRY(tmp.ensure((size_t)n * D * V * 2));
+        VX_HIP(hipMemcpy2DAsync(tmp.p, D * V * 2, e->d_dlog.p, V * 2, V * 2, n, hipMemcpyDeviceToDevice, st));
+        for (int64_t i = 1; i < D; i++)
+            VX_HIP(hipMemcpy2DAsync((uint16_t *)tmp.p + i * V, D * V * 2, (uint16_t *)e->d_dlog.p + (size_t)i * n * V,
+                                    V * 2, V * 2, n, hipMemcpyDeviceToDevice, st));
+        VX_TRY(stochastic_accept_launch(e->d_tlog.p, tmp.p, VX_BF16, cand, uni, (int32_t *)e->d_acc.p,
+                                        (uint32_t *)e->d_tok.p, n, D, V, e->temperature, e->d_argws.p, e->d_argws.n,
+                                        st));
+        VX_HIP(hipStreamSynchronize(st));
+    }
+    // ---- results to host (one copy set, one sync)
+    uint8_t *hr = hs + total + small;
+    int32_t *h_acc = (int32_t *)hr;
+    uint32_t *h_tok = (uint32_t *)(hr + n * 4);
+    uint32_t *h_cand = h_tok + n * (D + 1);
+    VX_HIP(hipMemcpyAsync(h_acc, e->d_acc.p, n * 4, hipMemcpyDeviceToHost, st));
+    VX_HIP(hipMemcpyAsync(h_tok, e->d_tok.p, n * (D + 1) * 4, hipMemcpyDeviceToHost, st));
+    VX_HIP(hipMemcpyAsync(h_cand, cand, n * D * 4, hipMemcpyDeviceToHost, st));
+    if (prof) VX_HIP(hipEventRecord(e->ev[3], st));
+    VX_HIP(hipStreamSynchronize(st));
+    if (prof) {
+        vx_step_profile &pp = e->last_prof;
+        pp = vx_step_profile{};
+        float ms = 0.f;
+        VX_HIP(hipEventElapsedTime(&ms, e->ev[0], e->ev[1]));
+        pp.draft_ms = ms;
+        VX_HIP(hipEventElapsedTime(&ms, e->ev[1], e->ev[2]));
+        pp.verify_ms = ms;
+        VX_HIP(hipEventElapsedTime(&ms, e->ev[2], e->ev[3]));
+        pp.accept_ms = ms;
+        for (auto *pr : {&e->prof_verify, &e->prof_draft}) {
+            const bool ver = pr == &e->prof_verify;
+            for (const auto &r : pr->recs) {
+                VX_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+                if (ver) {
+                    pp.verify_kernel_ms[r.cls] += ms;
+                    pp.verify_kernel_bytes[r.cls] += r.bytes;
+                    pp.verify_kernel_launches[r.cls] += 1;
+                } else {
+                    pp.draft_kernel_ms[r.cls] += ms;
+                    pp.draft_kernel_bytes[r.cls] += r.bytes;
+                    pp.draft_kernel_launches[r.cls] += 1;
+                }
+            }
+        }
+    }
+    e->last_n = n;
+    e->last_k = D;
+    e->last_cand.assign(h_cand, h_cand + n * D);
+    // ---- commit (spec.rs:294-309)
+    for (int64_t b = 0; b < n; b++) {
+        SpecState &s = *S[b];
+        const int32_t a = h_acc[b];
+        VX_REQUIRE(a >= 0 && a <= D, "step: acceptance returned an invalid count");
+        for (int32_t i = 0; i <= a; i++) committed[b * (D + 1) + i] = h_tok[b * (D + 1) + i];
+        if (e->fix_hole && a == D) {
+            // opt-in: feed c[D-1] to the draft so its KV has no unwritten slot
+            VX_TRY(ensure_capacity(e->dp, s.draft_blocks, (s.kv_len + D + 1 + ps - 1) / ps, "grow draft block table"));
+            vx_seq_slice one = {1, s.kv_len + D, s.draft_blocks.data(), (int64_t)s.draft_blocks.size()};
+            DevBuf lg;
+            VX_TRY(lg.ensure((size_t)V * 2));
+            const uint32_t id = h_cand[b * D + D - 1];
+            VX_TRY(vx_forward(e->draft, e->dp, &id, &one, 1, 0, nullptr, lg.p, stream));
+        }
+        s.kv_len += a + 1;
+        s.last_token = h_tok[b * (D + 1) + a];
+        s.tokens.insert(s.tokens.end(), h_tok + b * (D + 1), h_tok + b * (D + 1) + a + 1);
+        s.round++;
+        int stop = 0;
+        if (eos >= 0)
+            for (int32_t i = 0; i <= a; i++)
+                if (h_tok[b * (D + 1) + i] == (uint32_t)eos) stop = 1;
+        outcomes[b] = {a, a + 1, stop};
+    }
+    return 0;
+}
+
+extern "C" int64_t vx_spec_state_kv_len(const vx_spec *e, int64_t s) {
+    if (!e || s < 0 || s >= (int64_t)e->states.size()) return -1;
+    return e->states[s].kv_len;
+}
+extern "C" int64_t vx_spec_state_num_tokens(const vx_spec *e, int64_t s) {
+    if (!e || s < 0 || s >= (int64_t)e->states.size()) return -1;
+    return (int64_t)e->states[s].tokens.size();
+}
+extern "C" int vx_spec_state_tokens(const vx_spec *e, int64_t s, uint32_t *out, int64_t cap) {
+    VX_REQUIRE(e && s >= 0 && s < (int64_t)e->states.size() && out, "state: bad argument");
+    const auto &t = e->states[s].tokens;
+    VX_REQUIRE(cap >= (int64_t)t.size(), "state: output too small");
+    memcpy(out, t.data(), t.size() * 4);
+    return 0;
+}
+extern "C" int vx_spec_last_trace(const vx_spec *e, uint32_t *candidates, float *verify_logits) {
+    VX_REQUIRE(e && e->last_n > 0, "trace: no step yet");
+    if (candidates) memcpy(candidates, e->last_cand.data(), e->last_cand.size() * 4);
+    if (verify_logits) {
+        const int64_t n = e->last_n * (e->last_k + 1) * e->target->cfg.vocab;
+        std::vector<uint16_t> tmp((size_t)n);
+        VX_HIP(hipMemcpy(tmp.data(), e->d_tlog.p, (size_t)n * 2, hipMemcpyDeviceToHost));
+        for (int64_t i = 0; i < n; i++) verify_logits[i] = bf2f(tmp[i]);
+    }
+    return 0;
+}
+extern "C" int vx_spec_set_profiling(vx_spec *e, int enable) {
+    VX_REQUIRE(e, "profiling: null engine");
+    e->profiling = enable != 0;
+    return 0;
+}
+extern "C" int vx_spec_last_profile(const vx_spec *e, vx_step_profile *out) {
+    VX_REQUIRE(e && out, "profiling: null argument");
+    VX_REQUIRE(e->profiling, "profiling: not enabled");
+    *out = e->last_prof;
+    return 0;
+}
+extern "C" void vx_spec_free(vx_spec *e, int64_t s) {
+    if (!e || s < 0 || s >= (int64_t)e->states.size() || !e->states[s].live) return;
+    SpecState &st = e->states[s];
+    vx_pages_free(e->tp, st.target_blocks.data(), (int64_t)st.target_blocks.size());
+    vx_pages_free(e->dp, st.draft_blocks.data(), (int64_t)st.draft_blocks.size());
+    st = SpecState{};
+}
+
+extern "C" const char *vx_last_error(void) { return g_err.c_str(); }
+extern "C" const char *vx_version(void) { return "velox_amd 0.1.0 (gfx950)"; }

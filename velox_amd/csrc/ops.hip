@@ -1,0 +1,782 @@
+// Row-wise kernels of the verify path, gfx950: embedding, RMSNorm, fused
+// q/k-norm + RoPE + KV write, the RoPE / scatter drop-ins, and acceptance.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "vx_common.h"
+
+namespace vx {
+
+// ===========================================================================
+// embedding + norms (qwen3.rs:998, :393-394, :923-928, :965; candle RmsNorm)
+// ===========================================================================
+
+// h[r, :] = round_T(embed[ids[r], :]); embed is stored in T already.
+__global__ void embed_kernel(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_t H,
+                             int64_t vocab) {
+    const int64_t r = blockIdx.x;
+    uint32_t id = ids[r];
+    if (id >= (uint32_t)vocab) id = (uint32_t)(vocab - 1);
+    const uint4 *src = (const uint4 *)(embed + (int64_t)id * H);
+    uint4 *dst = (uint4 *)(h + r * H);
+    for (int64_t i = threadIdx.x; i < H / 8; i += blockDim.x) dst[i] = src[i];
+}
+
+// y = round_bf16(x / sqrt(mean(x^2) + eps) * w), stored as f16 (exact carrier
+// of the bf16 value) for the next GEMM.  x, w in bf16.  rows optionally
+// gathered through row_idx (last row per sequence).
+__global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const uint16_t *x, const uint16_t *w,
+                                                          uint16_t *y, const uint32_t *row_idx,
+                                                          int64_t H, float eps, int out_dt) {
+    __shared__ float red[256];
+    const int64_t r = blockIdx.x;
+    const int64_t src_r = row_idx ? row_idx[r] : r;
+    const uint16_t *xr = x + src_r * H;
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < H; i += 256) {
+        const float v = bf16_bits_to_f32(xr[i]);
+        s += v * v;
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
+        __syncthreads();
+    }
+    const float m = sqrtf(red[0] / (float)H + eps);
+    for (int64_t i = threadIdx.x; i < H; i += 256) {
+        const float v = round_to<VX_BF16>(bf16_bits_to_f32(xr[i]) / m * bf16_bits_to_f32(w[i]));
+        if (out_dt == VX_F16)
+            y[r * H + i] = f32_to_f16_bits(v);
+        else
+            y[r * H + i] = f32_to_bf16_bits(v);
+    }
+}
+
+// Per row: q/k heads get the per-head RMSNorm (qwen3.rs:435-454) and RoPE at
+// rope_pos[row] (MSL :209-241, tables in bf16); q goes to qout and k, v are
+// written into the pools at (page_ids[row], slots[row]) (MSL :251-279), all in
+// the pool dtype (f16 pools carry the bf16-rounded values exactly).  One wave
+// per head.
+__global__ __launch_bounds__(256) void qk_rope_scatter_kernel(
+    const uint16_t *qkv, const uint16_t *qn_w, const uint16_t *kn_w, const uint16_t *cos_t,
+    const uint16_t *sin_t, const uint32_t *rope_pos, const uint32_t *page_ids,
+    const uint32_t *slots, uint16_t *qout, uint16_t *k_pool, uint16_t *v_pool, int HQ, int HK,
+    int D, int ps, float eps, int kv_dt) {
+    const int64_t r = blockIdx.x;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int QW = HQ * D, KW = HK * D;
+    const uint16_t *row = qkv + r * (int64_t)(QW + 2 * KW);
+    const int half = D / 2;
+    const uint32_t pos = rope_pos[r];
+    const int64_t page = page_ids[r];
+    const int slot = (int)slots[r];
+    for (int h = wave; h < HQ + 2 * HK; h += 4) {
+        if (h >= HQ + HK) {  // v head: plain copy
+            const int hv = h - HQ - HK;
+            const uint16_t *src = row + QW + KW + hv * D;
+            uint16_t *dst = v_pool + ((page * HK + hv) * ps + slot) * (int64_t)D;
+            for (int i = lane; i < D; i += 64) {
+                const float v = bf16_bits_to_f32(src[i]);
+                dst[i] = kv_dt == VX_F16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
+            }
+            continue;
+        }
+        const bool is_q = h < HQ;
+        const uint16_t *src = is_q ? row + h * D : row + QW + (h - HQ) * D;
+        const uint16_t *nw = is_q ? qn_w : kn_w;
+        // per-head RMSNorm over D
+        float ss = 0.f;
+        for (int i = lane; i < D; i += 64) {
+            const float v = bf16_bits_to_f32(src[i]);
+            ss += v * v;
+        }
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        const float m = sqrtf(ss / (float)D + eps);
+        uint16_t *dst = is_q ? qout + (r * HQ + h) * (int64_t)D
+                             : k_pool + ((page * HK + (h - HQ)) * ps + slot) * (int64_t)D;
+        for (int j = lane; j < half; j += 64) {
+            const float x1 = round_to<VX_BF16>(bf16_bits_to_f32(src[j]) / m * bf16_bits_to_f32(nw[j]));
+            const float x2 = round_to<VX_BF16>(bf16_bits_to_f32(src[j + half]) / m * bf16_bits_to_f32(nw[j + half]));
+            const float c = bf16_bits_to_f32(cos_t[(int64_t)pos * half + j]);
+            const float s = bf16_bits_to_f32(sin_t[(int64_t)pos * half + j]);
+            const float y1 = round_to<VX_BF16>(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
+            const float y2 = round_to<VX_BF16>(__fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c)));
+            if (kv_dt == VX_F16) {
+                dst[j] = f32_to_f16_bits(y1);
+                dst[j + half] = f32_to_f16_bits(y2);
+            } else {
+                dst[j] = f32_to_bf16_bits(y1);
+                dst[j + half] = f32_to_bf16_bits(y2);
+            }
+        }
+    }
+}
+
+// ===========================================================================
+// drop-in RoPE / scatter (metal_kernels.rs MSL :209-241, :251-279)
+// ===========================================================================
+template <int DT>
+__global__ void rope_kernel(void *x, const void *cos_t, const void *sin_t, const uint32_t *offsets,
+                            int64_t n, int64_t h, int64_t half) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t tot = n * h * half;
+    if (idx >= tot) return;
+    const int64_t dp = idx % half;
+    const int64_t hh = (idx / half) % h;
+    const int64_t r = idx / (half * h);
+    const int64_t off = offsets[r];
+    const int64_t base = (r * h + hh) * 2 * half;
+    const float x1 = ld_elem<DT>(x, base + dp);
+    const float x2 = ld_elem<DT>(x, base + dp + half);
+    const float c = ld_elem<DT>(cos_t, off * half + dp);
+    const float s = ld_elem<DT>(sin_t, off * half + dp);
+    st_elem<DT>(x, base + dp, __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
+    st_elem<DT>(x, base + dp + half, __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c)));
+}
+
+__global__ void scatter_kernel(uint8_t *pool, const uint8_t *values, const uint32_t *page_ids,
+                               const uint32_t *slots, int64_t n, int64_t h, int64_t ps,
+                               int64_t row_bytes, int64_t num_pages) {
+    // one block per (row, head); row_bytes = d * elem
+    const int64_t r = blockIdx.x / h;
+    const int64_t hh = blockIdx.x % h;
+    const int64_t page = page_ids[r];
+    const int64_t slot = slots[r];
+    if (page >= num_pages || slot >= ps) return;
+    const uint8_t *src = values + (r * h + hh) * row_bytes;
+    uint8_t *dst = pool + ((page * h + hh) * ps + slot) * row_bytes;
+    for (int64_t i = threadIdx.x * 4; i < row_bytes; i += blockDim.x * 4)
+        *(uint32_t *)(dst + i) = *(const uint32_t *)(src + i);
+}
+
+// ===========================================================================
+// argmax / acceptance
+// ===========================================================================
+constexpr int kArgChunk = 8192;
+constexpr int kSmThreads = 256;
+constexpr int kSmChunk = 8192;  // softmax statistics chunk (matches the host definition)
+constexpr int kSmSub = 256;     // residual-sampling sub-chunk
+
+struct ArgBest {
+    float v;
+    uint32_t i;
+};
+__device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
+    // larger value wins; equal values: smaller index; "none" is (-inf, ~0u)
+    if (b.v > a.v) return b;
+    if (a.v > b.v) return a;
+    return b.i < a.i ? b : a;
+}
+
+template <int DT>
+__device__ ArgBest chunk_argmax(const void *row, int64_t lo, int64_t hi, float *sv, uint32_t *si) {
+    ArgBest best = {-__builtin_inff(), 0xffffffffu};
+    for (int64_t j = lo + threadIdx.x; j < hi; j += blockDim.x) {
+        const float v = ld_elem<DT>(row, j);
+        if (v > best.v) {  // strict: the first (smallest) index per thread wins ties; NaN never wins
+            best.v = v;
+            best.i = (uint32_t)j;
+        }
+    }
+    sv[threadIdx.x] = best.v;
+    si[threadIdx.x] = best.i;
+    __syncthreads();
+    for (int st = blockDim.x / 2; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) {
+            ArgBest o = arg_better({sv[threadIdx.x], si[threadIdx.x]}, {sv[threadIdx.x + st], si[threadIdx.x + st]});
+            sv[threadIdx.x] = o.v;
+            si[threadIdx.x] = o.i;
+        }
+        __syncthreads();
+    }
+    ArgBest r = {sv[0], si[0]};
+    __syncthreads();
+    return r;
+}
+
+struct AcceptArgs {
+    const void *logits;
+    int64_t vocab;
+    int rows_per_group;  // rows belonging to one sequence
+    int n_chunks;        // argmax chunks per row
+    float *pv;           // partial values [rows, n_chunks]
+    uint32_t *pi;        // partial indices
+    int mode;            // 0 argmax rows, 1 greedy chain, 2 tree
+    const uint32_t *cand;  // chain: [B, k]; tree: node tokens [B, R]
+    int k;
+    int32_t *accepted;
+    uint32_t *tokens;    // chain: [B, k+1]; tree: [B, R]
+    int32_t *path;       // tree: [B, R]
+    uint32_t *argmax_out;  // optional [rows]
+    uint32_t *next_ids;    // optional (mode 0): argmax also written here ([rows], stride next_stride)
+    int64_t next_stride;
+    int parents[64];
+};
+
+// Pass 1: (max, first index) of every 8192-wide chunk of every row.
+template <int DT>
+__global__ __launch_bounds__(256) void argmax_partial_kernel(AcceptArgs a) {
+    __shared__ float sv[256];
+    __shared__ uint32_t si[256];
+    const int64_t row = blockIdx.x / a.n_chunks;
+    const int chunk = blockIdx.x % a.n_chunks;
+    const int64_t lo = (int64_t)chunk * kArgChunk;
+    const int64_t hi = min(a.vocab, lo + kArgChunk);
+    const void *rowp = (const char *)a.logits + row * a.vocab * (DT == VX_F32 ? 4 : 2);
+    const ArgBest cbest = chunk_argmax<DT>(rowp, lo, hi, sv, si);
+    if (threadIdx.x == 0) {
+        a.pv[row * a.n_chunks + chunk] = cbest.v;
+        a.pi[row * a.n_chunks + chunk] = cbest.i;
+    }
+}
+
+// Pass 2: one block per group (sequence): combine chunk partials of each row
+// in chunk order, then the acceptance walk on thread 0.
+__global__ __launch_bounds__(64) void accept_finish_kernel(AcceptArgs a) {
+    __shared__ uint32_t am[64];
+    const int64_t grp = blockIdx.x;
+    for (int rr = threadIdx.x; rr < a.rows_per_group; rr += blockDim.x) {
+        const int64_t rw = grp * a.rows_per_group + rr;
+        ArgBest best = {-__builtin_inff(), 0xffffffffu};
+        for (int c = 0; c < a.n_chunks; c++) best = arg_better(best, {a.pv[rw * a.n_chunks + c], a.pi[rw * a.n_chunks + c]});
+        const uint32_t idx = best.i == 0xffffffffu ? 0u : best.i;
+        if (rr < 64) am[rr] = idx;
+        if (a.argmax_out) a.argmax_out[rw] = idx;
+        if (a.mode == 0 && a.next_ids) a.next_ids[rw * a.next_stride] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0 || a.mode == 0) return;
+    const int64_t b = grp;
+    if (a.mode == 1) {  // spec.rs:284-292
+        int acc = 0;
+        while (acc < a.k && a.cand[b * a.k + acc] == am[acc]) acc++;
+        for (int i = 0; i < acc; i++) a.tokens[b * (a.k + 1) + i] = a.cand[b * a.k + i];
+        a.tokens[b * (a.k + 1) + acc] = am[acc];
+        a.accepted[b] = acc;
+    } else {  // tree walk from the root
+        const int R = a.rows_per_group;
+        int cur = 0, acc = 0;
+        a.path[b * R] = 0;
+        for (;;) {
+            const uint32_t t = am[cur];
+            int nxt = -1;
+            for (int j = cur + 1; j < R; j++)
+                if (a.parents[j] == cur && a.cand[b * R + j] == t) {
+                    nxt = j;
+                    break;
+                }
+            if (nxt < 0) break;
+            a.tokens[b * R + acc] = t;
+            acc++;
+            a.path[b * R + acc] = nxt;
+            cur = nxt;
+        }
+        a.tokens[b * R + acc] = am[cur];
+        a.accepted[b] = acc;
+    }
+}
+
+// ---- stochastic acceptance ------------------------------------------------
+// Row statistics with the fixed structure shared with the host definition:
+// per chunk of 8192, 256 strided thread partials folded by a stride-halving
+// tree; chunk (max, sum) pairs combined in chunk order by the consumer.
+template <int DT>
+__global__ __launch_bounds__(256) void softmax_stats_kernel(const void *logits, int64_t vocab,
+                                                            float inv_t, float *cm, float *cz,
+                                                            int n_chunks) {
+    __shared__ float red[256];
+    const int64_t row = blockIdx.x / n_chunks;
+    const int chunk = blockIdx.x % n_chunks;
+    const int64_t lo = (int64_t)chunk * kSmChunk;
+    const int64_t hi = min(vocab, lo + kSmChunk);
+    const void *r = (const char *)logits + row * vocab * (DT == VX_F32 ? 4 : 2);
+    float m = -__builtin_inff();
+    for (int64_t j = lo + threadIdx.x; j < hi; j += 256) m = fmaxf(m, ld_elem<DT>(r, j));
+    red[threadIdx.x] = m;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
+        __syncthreads();
+    }
+    m = red[0];
+    __syncthreads();
+    float s = 0.f;
+    for (int64_t j = lo + threadIdx.x; j < hi; j += 256) s = __fadd_rn(s, vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(r, j), m), inv_t)));
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) red[threadIdx.x] = __fadd_rn(red[threadIdx.x], red[threadIdx.x + st]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        cm[row * n_chunks + chunk] = m;
+        cz[row * n_chunks + chunk] = red[0];
+    }
+}
+
+__device__ __forceinline__ void combine_stats(const float *cm, const float *cz, int n_chunks,
+                                              float inv_t, float &M, float &Z) {
+    M = -__builtin_inff();
+    for (int c = 0; c < n_chunks; c++) M = fmaxf(M, cm[c]);
+    Z = 0.f;
+    for (int c = 0; c < n_chunks; c++)
+        Z = __fadd_rn(Z, __fmul_rn(cz[c], vx_detexp(__fmul_rn(__fsub_rn(cm[c], M), inv_t))));
+}
+
+template <int DT>
+__device__ __forceinline__ float resid_elem(const void *lt, float mt, float zt, const void *ld,
+                                            float md, float zd, float inv_t, int64_t j) {
+    const float p = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(lt, j), mt), inv_t)), zt);
+    if (!ld) return p;
+    const float q = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(ld, j), md), inv_t)), zd);
+    const float d = __fsub_rn(p, q);
+    return d > 0.f ? d : 0.f;
+}
+
+// Inverse-CDF draw over r_j (hierarchical prefix order: chunk -> sub-chunk ->
+// element, each level summed sequentially in index order).  Called by a full
+// 256-thread block; sub-chunk sums use block-wide parallelism (one sub-chunk
+// per thread at a time), the walk itself runs on thread 0.
+template <int DT>
+__device__ uint32_t sample_residual_block(const void *lt, float mt, float zt, const void *ld, float md,
+                                          float zd, int64_t vocab, float inv_t, float u, float *ss,
+                                          float *cs, int *s_last_pos, uint32_t *s_out) {
+    const int64_t nch = (vocab + kSmChunk - 1) / kSmChunk;
+    const int64_t nsub_per = kSmChunk / kSmSub;
+    const int64_t nsub = nch * nsub_per;
+    if (threadIdx.x == 0) *s_last_pos = -1;
+    __syncthreads();
+    int my_last = -1;
+    for (int64_t sidx = threadIdx.x; sidx < nsub; sidx += blockDim.x) {
+        const int64_t lo = sidx * kSmSub;
+        float s = 0.f;
+        for (int64_t j = lo; j < lo + kSmSub && j < vocab; j++) {
+            const float r = resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j);
+            if (r > 0.f) my_last = (int)j;
+            s = __fadd_rn(s, r);
+        }
+        ss[sidx] = s;
+    }
+    atomicMax(s_last_pos, my_last);
+    __syncthreads();
+    for (int64_t c = threadIdx.x; c < nch; c += blockDim.x) {
+        float s = 0.f;
+        for (int64_t i = 0; i < nsub_per; i++) s = __fadd_rn(s, ss[c * nsub_per + i]);
+        cs[c] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float total = 0.f;
+        for (int64_t c = 0; c < nch; c++) total = __fadd_rn(total, cs[c]);
+        const float target = __fmul_rn(u, total);
+        uint32_t result = *s_last_pos < 0 ? 0u : (uint32_t)*s_last_pos;
+        float run = 0.f;
+        for (int64_t c = 0; c < nch; c++) {
+            if (__fadd_rn(run, cs[c]) > target) {
+                int64_t found = -1;
+                float run2 = run;
+                for (int64_t i = 0; i < nsub_per && found < 0; i++) {
+                    const int64_t sidx = c * nsub_per + i;
+                    if (__fadd_rn(run2, ss[sidx]) > target) {
+                        float run3 = run2;
+                        const int64_t lo = sidx * kSmSub;
+                        for (int64_t j = lo; j < lo + kSmSub && j < vocab; j++) {
+                            run3 = __fadd_rn(run3, resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j));
+                            if (run3 > target) {
+                                found = j;
+                                break;
+                            }
+                        }
+                        if (found < 0) {
+                            for (int64_t j = (c + 1) * kSmChunk - 1; j >= c * kSmChunk; j--)
+                                if (j < vocab && resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j) > 0.f) {
+                                    found = j;
+                                    break;
+                                }
+                        }
+                        break;
+                    }
+                    run2 = __fadd_rn(run2, ss[sidx]);
+                }
+                if (found < 0) {
+                    for (int64_t j = (c + 1) * kSmChunk - 1; j >= c * kSmChunk; j--)
+                        if (j < vocab && resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j) > 0.f) {
+                            found = j;
+                            break;
+                        }
+                }
+                if (found >= 0) result = (uint32_t)found;
+                break;
+            }
+            run = __fadd_rn(run, cs[c]);
+        }
+        *s_out = result;
+    }
+    __syncthreads();
+    return *s_out;
+}
+
+constexpr int kMaxSub = 1024;  // supports vocab <= kMaxSub * kSmSub = 262144
+constexpr int kMaxChunks = kMaxSub / (kSmChunk / kSmSub);
+
+// One block per sequence: accept/reject walk + residual or bonus draw.
+template <int DT>
+__global__ __launch_bounds__(256) void stochastic_accept_kernel(
+    const void *tl, const void *dl, const uint32_t *cand, const float *uni, const float *cm_t,
+    const float *cz_t, const float *cm_d, const float *cz_d, int n_chunks, int64_t vocab, int k,
+    float inv_t, int32_t *accepted, uint32_t *tokens) {
+    __shared__ float ss[kMaxSub];
+    __shared__ float cs[kMaxChunks];
+    __shared__ int s_last_pos;
+    __shared__ uint32_t s_out;
+    __shared__ int s_rej;
+    __shared__ float s_stats[4];
+    const int64_t b = blockIdx.x;
+    const size_t esz = DT == VX_F32 ? 4 : 2;
+    int a = 0;
+    for (; a < k; a++) {
+        const int64_t trow = b * (k + 1) + a;
+        const int64_t drow = b * k + a;
+        if (threadIdx.x == 0) {
+            float mt, zt, md, zd;
+            combine_stats(cm_t + trow * n_chunks, cz_t + trow * n_chunks, n_chunks, inv_t, mt, zt);
+            combine_stats(cm_d + drow * n_chunks, cz_d + drow * n_chunks, n_chunks, inv_t, md, zd);
+            const uint32_t c = cand[b * k + a];
+            const float p = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>((const char *)tl + trow * vocab * esz, c), mt), inv_t)), zt);
+            const float q = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>((const char *)dl + drow * vocab * esz, c), md), inv_t)), zd);
+            const float ratio = __fdiv_rn(p, q);
+            const float acc = ratio < 1.0f ? ratio : 1.0f;
+            const float u = uni[(b * (k + 1) + a) * 4 + 1];
+            s_rej = !(u < acc);
+            s_stats[0] = mt;
+            s_stats[1] = zt;
+            s_stats[2] = md;
+            s_stats[3] = zd;
+            if (!s_rej) tokens[b * (k + 1) + a] = c;
+        }
+        __syncthreads();
+        if (s_rej) {
+            const uint32_t nxt = sample_residual_block<DT>(
+                (const char *)tl + trow * vocab * esz, s_stats[0], s_stats[1],
+                (const char *)dl + drow * vocab * esz, s_stats[2], s_stats[3], vocab, inv_t,
+                uni[(b * (k + 1) + a) * 4 + 2], ss, cs, &s_last_pos, &s_out);
+            if (threadIdx.x == 0) {
+                tokens[b * (k + 1) + a] = nxt;
+                accepted[b] = a;
+            }
+            return;
+        }
+        __syncthreads();
+    }
+    const int64_t trow = b * (k + 1) + k;
+    if (threadIdx.x == 0) {
+        float mt, zt;
+        combine_stats(cm_t + trow * n_chunks, cz_t + trow * n_chunks, n_chunks, inv_t, mt, zt);
+        s_stats[0] = mt;
+        s_stats[1] = zt;
+    }
+    __syncthreads();
+    const uint32_t nxt = sample_residual_block<DT>((const char *)tl + trow * vocab * esz, s_stats[0], s_stats[1],
+                                                   nullptr, 0.f, 1.f, vocab, inv_t,
+                                                   uni[(b * (k + 1) + k) * 4 + 2], ss, cs, &s_last_pos, &s_out);
+    if (threadIdx.x == 0) {
+        tokens[b * (k + 1) + k] = nxt;
+        accepted[b] = k;
+    }
+}
+
+// One block per row: draw from softmax(row / T) with uniforms[row * stride].
+template <int DT>
+__global__ __launch_bounds__(256) void sample_rows_kernel(const void *logits, const float *uni,
+                                                          int64_t ustride, const float *cm,
+                                                          const float *cz, int n_chunks,
+                                                          int64_t vocab, float inv_t,
+                                                          uint32_t *out, uint32_t *next_ids,
+                                                          int64_t next_stride) {
+    __shared__ float ss[kMaxSub];
+    __shared__ float cs[kMaxChunks];
+    __shared__ int s_last_pos;
+    __shared__ uint32_t s_out;
+    __shared__ float s_st[2];
+    const int64_t row = blockIdx.x;
+    if (threadIdx.x == 0) {
+        float M, Z;
+        combine_stats(cm + row * n_chunks, cz + row * n_chunks, n_chunks, inv_t, M, Z);
+        s_st[0] = M;
+        s_st[1] = Z;
+    }
+    __syncthreads();
+    const size_t esz = DT == VX_F32 ? 4 : 2;
+    const uint32_t t = sample_residual_block<DT>((const char *)logits + row * vocab * esz, s_st[0], s_st[1],
+                                                 nullptr, 0.f, 1.f, vocab, inv_t, uni[row * ustride],
+                                                 ss, cs, &s_last_pos, &s_out);
+    if (threadIdx.x == 0) {
+        out[row] = t;
+        if (next_ids) next_ids[row * next_stride] = t;
+    }
+}
+
+}  // namespace vx
+
+using namespace vx;
+
+namespace vx {
+
+constexpr size_t kAccCounterBytes = 65536;
+
+size_t accept_workspace_bytes(int64_t rows, int64_t vocab) {
+    const int64_t nch = vx_cdiv(vocab, kArgChunk);
+    return kAccCounterBytes + (size_t)rows * nch * 8 * 2 + 256;
+}
+
+int argmax_accept_launch(const void *logits, int ldt, int64_t rows, int64_t vocab, int mode,
+                         int rows_per_group, const uint32_t *cand, int k, int32_t *accepted,
+                         uint32_t *tokens, int32_t *path, const int32_t *parents, uint32_t *argmax_out,
+                         uint32_t *next_ids, int64_t next_stride, void *ws, size_t ws_bytes,
+                         hipStream_t st) {
+    VX_REQUIRE(vocab > 0 && rows > 0, "argmax: empty logits");
+    AcceptArgs a{};
+    a.logits = logits;
+    a.vocab = vocab;
+    a.rows_per_group = rows_per_group;
+    a.n_chunks = (int)vx_cdiv(vocab, kArgChunk);
+    const size_t need = accept_workspace_bytes(rows, vocab);
+    if (!ws) {
+        VX_TRY(stream_workspace(st, need, &ws));
+    } else if (ws_bytes < need) {
+        return set_error("accept: workspace too small");
+    }
+    VX_REQUIRE(rows_per_group >= 1 && rows_per_group <= 64 && rows % rows_per_group == 0,
+               "accept: rows per sequence must be 1..64");
+    a.pv = (float *)((char *)ws + kAccCounterBytes);
+    a.pi = (uint32_t *)((char *)a.pv + (size_t)rows * a.n_chunks * 4);
+    a.mode = mode;
+    a.cand = cand;
+    a.k = k;
+    a.accepted = accepted;
+    a.tokens = tokens;
+    a.path = path;
+    a.argmax_out = argmax_out;
+    a.next_ids = next_ids;
+    a.next_stride = next_stride;
+    if (parents)
+        for (int i = 0; i < rows_per_group && i < 64; i++) a.parents[i] = parents[i];
+    dim3 grid((unsigned)(rows * a.n_chunks));
+    if (ldt == VX_BF16)
+        hipLaunchKernelGGL(argmax_partial_kernel<VX_BF16>, grid, dim3(256), 0, st, a);
+    else if (ldt == VX_F16)
+        hipLaunchKernelGGL(argmax_partial_kernel<VX_F16>, grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL(argmax_partial_kernel<VX_F32>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(accept_finish_kernel, dim3((unsigned)(rows / rows_per_group)), dim3(64), 0, st, a);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+// Statistics live after the arrival-counter region so that argmax / accept
+// launches sharing the same workspace keep their zeroed counters.
+size_t stochastic_workspace_bytes(int64_t rows, int64_t vocab) {
+    return kAccCounterBytes + (size_t)rows * vx_cdiv(vocab, kSmChunk) * 8 + 256;
+}
+
+template <int DT>
+static void launch_stats(const void *lg, int64_t rows, int64_t vocab, float inv_t, float *cm, float *cz,
+                         int nch, hipStream_t st) {
+    hipLaunchKernelGGL(softmax_stats_kernel<DT>, dim3((unsigned)(rows * nch)), dim3(256), 0, st, lg, vocab,
+                       inv_t, cm, cz, nch);
+}
+
+static void stats(const void *lg, int ldt, int64_t rows, int64_t vocab, float inv_t, float *cm,
+                  float *cz, int nch, hipStream_t st) {
+    if (ldt == VX_BF16)
+        launch_stats<VX_BF16>(lg, rows, vocab, inv_t, cm, cz, nch, st);
+    else if (ldt == VX_F16)
+        launch_stats<VX_F16>(lg, rows, vocab, inv_t, cm, cz, nch, st);
+    else
+        launch_stats<VX_F32>(lg, rows, vocab, inv_t, cm, cz, nch, st);
+}
+
+int sample_rows_launch(const void *logits, int ldt, const float *uni, int64_t ustride, uint32_t *out,
+                       int64_t rows, int64_t vocab, float temperature, uint32_t *next_ids,
+                       int64_t next_stride, void *ws, size_t ws_bytes, hipStream_t st) {
+    VX_REQUIRE(temperature > 0.f, "sample: temperature must be > 0");
+    VX_REQUIRE(vocab <= (int64_t)kMaxSub * kSmSub, "sample: vocab too large");
+    const int nch = (int)vx_cdiv(vocab, kSmChunk);
+    const size_t need = stochastic_workspace_bytes(rows, vocab);
+    if (!ws) {
+        VX_TRY(stream_workspace(st, need, &ws));
+    } else if (ws_bytes < need) {
+        return set_error("sample: workspace too small");
+    }
+    float *cm = (float *)((char *)ws + kAccCounterBytes);
+    float *cz = cm + rows * nch;
+    const float inv_t = 1.0f / temperature;
+    stats(logits, ldt, rows, vocab, inv_t, cm, cz, nch, st);
+    if (ldt == VX_BF16)
+        hipLaunchKernelGGL(sample_rows_kernel<VX_BF16>, dim3((unsigned)rows), dim3(256), 0, st, logits, uni, ustride, cm, cz, nch, vocab, inv_t, out, next_ids, next_stride);
+    else if (ldt == VX_F16)
+        hipLaunchKernelGGL(sample_rows_kernel<VX_F16>, dim3((unsigned)rows), dim3(256), 0, st, logits, uni, ustride, cm, cz, nch, vocab, inv_t, out, next_ids, next_stride);
+    else
+        hipLaunchKernelGGL(sample_rows_kernel<VX_F32>, dim3((unsigned)rows), dim3(256), 0, st, logits, uni, ustride, cm, cz, nch, vocab, inv_t, out, next_ids, next_stride);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint32_t *cand,
+                             const float *uni, int32_t *accepted, uint32_t *tokens, int64_t batch,
+                             int64_t k, int64_t vocab, float temperature, void *ws, size_t ws_bytes,
+                             hipStream_t st) {
+    VX_REQUIRE(temperature > 0.f, "accept_stochastic: temperature must be > 0");
+    VX_REQUIRE(k >= 1, "accept_stochastic: k must be >= 1");
+    VX_REQUIRE(vocab <= (int64_t)kMaxSub * kSmSub, "accept_stochastic: vocab too large");
+    const int nch = (int)vx_cdiv(vocab, kSmChunk);
+    const int64_t trows = batch * (k + 1), drows = batch * k;
+    const size_t need = stochastic_workspace_bytes(trows + drows, vocab);
+    if (!ws) {
+        VX_TRY(stream_workspace(st, need, &ws));
+    } else if (ws_bytes < need) {
+        return set_error("accept_stochastic: workspace too small");
+    }
+    float *cm_t = (float *)((char *)ws + kAccCounterBytes);
+    float *cz_t = cm_t + trows * nch;
+    float *cm_d = cz_t + trows * nch;
+    float *cz_d = cm_d + drows * nch;
+    const float inv_t = 1.0f / temperature;
+    stats(tl, ldt, trows, vocab, inv_t, cm_t, cz_t, nch, st);
+    stats(dl, ldt, drows, vocab, inv_t, cm_d, cz_d, nch, st);
+    if (ldt == VX_BF16)
+        hipLaunchKernelGGL(stochastic_accept_kernel<VX_BF16>, dim3((unsigned)batch), dim3(256), 0, st, tl, dl, cand, uni, cm_t, cz_t, cm_d, cz_d, nch, vocab, (int)k, inv_t, accepted, tokens);
+    else if (ldt == VX_F16)
+        hipLaunchKernelGGL(stochastic_accept_kernel<VX_F16>, dim3((unsigned)batch), dim3(256), 0, st, tl, dl, cand, uni, cm_t, cz_t, cm_d, cz_d, nch, vocab, (int)k, inv_t, accepted, tokens);
+    else
+        hipLaunchKernelGGL(stochastic_accept_kernel<VX_F32>, dim3((unsigned)batch), dim3(256), 0, st, tl, dl, cand, uni, cm_t, cz_t, cm_d, cz_d, nch, vocab, (int)k, inv_t, accepted, tokens);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+// ---- engine helpers --------------------------------------------------------
+int embed_launch(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_t rows, int64_t H,
+                 int64_t vocab, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)rows), dim3(64), 0, st, ids, embed, h, H, vocab);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
+                   int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st) {
+    hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, w, y, row_idx, H, eps, out_dt);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+int qk_rope_scatter_launch(const uint16_t *qkv, const uint16_t *qn, const uint16_t *kn,
+                           const uint16_t *cos_t, const uint16_t *sin_t, const uint32_t *pos,
+                           const uint32_t *pages, const uint32_t *slots, uint16_t *qout,
+                           uint16_t *kp, uint16_t *vp, int64_t rows, int HQ, int HK, int D, int ps,
+                           float eps, int kv_dt, hipStream_t st) {
+    hipLaunchKernelGGL(qk_rope_scatter_kernel, dim3((unsigned)rows), dim3(256), 0, st, qkv, qn, kn, cos_t,
+                       sin_t, pos, pages, slots, qout, kp, vp, HQ, HK, D, ps, eps, kv_dt);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace vx
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" int vx_rope_inplace(void *x, const void *cos_t, const void *sin_t, const uint32_t *offsets,
+                               int64_t n, int64_t h, int64_t d, int64_t max_pos, int dtype,
+                               void *stream) {
+    VX_REQUIRE(d % 2 == 0, "batched_rope_decode: D must be even");
+    VX_REQUIRE(x && cos_t && sin_t && offsets, "batched_rope_decode: null tensor");
+    VX_REQUIRE(max_pos > 0, "batched_rope_decode: empty tables");
+    (void)max_pos;
+    const int64_t tot = n * h * (d / 2);
+    if (tot == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    dim3 grid((unsigned)vx_cdiv(tot, 256));
+    if (dtype == VX_F32)
+        hipLaunchKernelGGL(rope_kernel<VX_F32>, grid, dim3(256), 0, st, x, cos_t, sin_t, offsets, n, h, d / 2);
+    else if (dtype == VX_F16)
+        hipLaunchKernelGGL(rope_kernel<VX_F16>, grid, dim3(256), 0, st, x, cos_t, sin_t, offsets, n, h, d / 2);
+    else if (dtype == VX_BF16)
+        hipLaunchKernelGGL(rope_kernel<VX_BF16>, grid, dim3(256), 0, st, x, cos_t, sin_t, offsets, n, h, d / 2);
+    else
+        return set_error("batched_rope_decode: unsupported dtype");
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int vx_kv_scatter(void *pool, const void *values, const uint32_t *page_ids,
+                             const uint32_t *slots, int64_t n, int64_t num_pages, int64_t h,
+                             int64_t page_size, int64_t d, int dtype, void *stream) {
+    VX_REQUIRE(pool && values && page_ids && slots, "batched_scatter: null tensor");
+    VX_REQUIRE(dtype == VX_F32 || dtype == VX_F16 || dtype == VX_BF16, "batched_scatter: unsupported dtype");
+    const int64_t esz = dtype == VX_F32 ? 4 : 2;
+    VX_REQUIRE((d * esz) % 4 == 0, "batched_scatter: row bytes must be a multiple of 4");
+    if (n == 0 || h == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)(n * h)), dim3(64), 0, st, (uint8_t *)pool,
+                       (const uint8_t *)values, page_ids, slots, n, h, page_size, d * esz, num_pages);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int vx_argmax_rows(const void *logits, uint32_t *out, int64_t rows, int64_t vocab,
+                              int logits_dtype, void *stream) {
+    VX_REQUIRE(logits && out, "argmax: null tensor");
+    if (rows == 0) return 0;
+    return argmax_accept_launch(logits, logits_dtype, rows, vocab, 0, 1, nullptr, 0, nullptr, nullptr,
+                                nullptr, nullptr, out, nullptr, 0, nullptr, 0, (hipStream_t)stream);
+}
+
+extern "C" int vx_accept_greedy(const void *logits, const uint32_t *candidates, int32_t *accepted,
+                                uint32_t *tokens, int64_t batch, int64_t k, int64_t vocab,
+                                int logits_dtype, void *stream) {
+    VX_REQUIRE(k >= 1, "draft_k must be >= 1");
+    VX_REQUIRE(logits && candidates && accepted && tokens, "accept_greedy: null tensor");
+    VX_REQUIRE(k + 1 <= 64, "accept_greedy: k too large");
+    if (batch == 0) return 0;
+    return argmax_accept_launch(logits, logits_dtype, batch * (k + 1), vocab, 1, (int)(k + 1), candidates,
+                                (int)k, accepted, tokens, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
+                                0, (hipStream_t)stream);
+}
+
+extern "C" int vx_accept_tree(const void *logits, const int32_t *parents, const uint32_t *node_tokens,
+                              int32_t *accepted, int32_t *path, uint32_t *tokens, int64_t batch,
+                              int64_t r, int64_t vocab, int logits_dtype, void *stream) {
+    VX_REQUIRE(r >= 1 && r <= 64, "accept_tree: 1..64 nodes");
+    VX_REQUIRE(parents && parents[0] < 0, "accept_tree: node 0 must be the root");
+    for (int64_t j = 1; j < r; j++)
+        VX_REQUIRE(parents[j] >= 0 && parents[j] < j, "accept_tree: parents[j] must precede j");
+    if (batch == 0) return 0;
+    return argmax_accept_launch(logits, logits_dtype, batch * r, vocab, 2, (int)r, node_tokens, 0, accepted,
+                                tokens, path, parents, nullptr, nullptr, 0, nullptr, 0, (hipStream_t)stream);
+}
+
+extern "C" int vx_accept_stochastic(const void *target_logits, const void *draft_logits,
+                                    const uint32_t *candidates, const float *uniforms, int32_t *accepted,
+                                    uint32_t *tokens, int64_t batch, int64_t k, int64_t vocab,
+                                    float temperature, int logits_dtype, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+    VX_REQUIRE(target_logits && draft_logits && candidates && uniforms && accepted && tokens,
+               "accept_stochastic: null tensor");
+    if (batch == 0) return 0;
+    return stochastic_accept_launch(target_logits, draft_logits, logits_dtype, candidates, uniforms, accepted,
+                                    tokens, batch, k, vocab, temperature, workspace, workspace_bytes,
+                                    (hipStream_t)stream);
+}
+
+extern "C" int vx_sample_rows(const void *logits, const float *uniforms, int64_t uniform_stride,
+                              uint32_t *out, int64_t rows, int64_t vocab, float temperature,
+                              int logits_dtype, void *workspace, size_t workspace_bytes, void *stream) {
+    VX_REQUIRE(logits && uniforms && out, "sample: null tensor");
+    if (rows == 0) return 0;
+    return sample_rows_launch(logits, logits_dtype, uniforms, uniform_stride, out, rows, vocab, temperature,
+                              nullptr, 0, workspace, workspace_bytes, (hipStream_t)stream);
+}

@@ -1,0 +1,198 @@
+"""Operator-level mirror of the reference's Metal kernels (src/paged/metal_kernels.rs),
+running the gfx950 kernels through the C ABI.
+
+Same names, argument meaning and failure conditions as the reference:
+tensors are torch tensors on the GPU (torch provides device memory and the
+current stream only), outputs are freshly allocated like the reference's
+`Tensor::zeros` outputs, and shape/dtype/contiguity violations raise
+VeloxError with the reference's messages.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import BF16, EPI_STORE, F16, F32, VeloxError, check, lib
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+
+def _dt(t: torch.Tensor, what: str) -> int:
+    if t.dtype not in _DT:
+        raise VeloxError(f"{what}: unsupported dtype {t.dtype}")
+    return _DT[t.dtype]
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise VeloxError(msg)
+
+
+def _contig(name: str, **ts) -> None:
+    for label, t in ts.items():
+        if t is not None and not t.is_contiguous():
+            raise VeloxError(f"{name}: {label} must be contiguous")
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def qmm_4bit(x, qweight, scales, biases, bias=None, group_size=64):
+    """qmm_4bit (metal_kernels.rs:2069-2076): Y[M,N] = X . deq(W)^T (+ bias)."""
+    _need(x.dim() == 2 and qweight.dim() == 2, "qmm_4bit: x and qweight must be 2-D")
+    m, k = x.shape
+    n, kp = qweight.shape
+    _need(k % 8 == 0, f"qmm_4bit: K={k} must be a multiple of 8")
+    _need(kp == k // 8, f"qmm_4bit: qweight dim1 {kp} != K/8 {k // 8} (K={k})")
+    _need(group_size != 0 and group_size % 8 == 0 and k % group_size == 0,
+          f"qmm_4bit: group_size={group_size} must be a multiple of 8 and divide K={k}")
+    kg = k // group_size
+    _need(tuple(scales.shape) == (n, kg) and tuple(biases.shape) == (n, kg),
+          f"qmm_4bit: scales {list(scales.shape)} / biases {list(biases.shape)} mismatch expected [{n},{kg}]")
+    _need(scales.dtype == x.dtype and biases.dtype == x.dtype, "qmm_4bit: scales/biases dtype must match X")
+    _need(qweight.dtype in (torch.int32, torch.uint32), "qmm_4bit: qweight must be U32")
+    if bias is not None:
+        _need(bias.dim() == 1 and bias.shape[0] == n and bias.dtype == x.dtype,
+              f"qmm_4bit: bias must be [N={n}] of same dtype as X")
+    _contig("qmm_4bit", x=x, qweight=qweight, scales=scales, biases=biases, bias=bias)
+    y = torch.zeros((m, n), dtype=x.dtype, device=x.device)
+    check(lib.vx_qmm_4bit(x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                          _p(bias), y.data_ptr(), m, n, k, group_size, _dt(x, "qmm_4bit"), _stream()))
+    return y
+
+
+def qmm_4bit_ex(x, qweight, scales, biases, out, residual=None, x_shift=0, round_dtype=BF16,
+                epilogue=EPI_STORE, workspace=None):
+    """Fused-epilogue int4 GEMM used by the verify forward (f16 X, f16 affine params)."""
+    m, k = x.shape
+    n = qweight.shape[0]
+    ws = _p(workspace)
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(lib.vx_qmm_4bit_ex(x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                             out.data_ptr(), _p(residual), m, n, k, 64, x_shift, round_dtype,
+                             _DT[out.dtype], epilogue, ws, wsb, _stream()))
+    return out
+
+
+def paged_prefill_attention(q, k_pool, v_pool, block_table, cu_seqlens, seq_id_per_q, kv_offsets, scale,
+                            sliding_window=0, tree_mask=None):
+    """paged_prefill_attention (metal_kernels.rs:1680-1690), plus an optional per-row
+    tree mask (uint64 [total_q]) for tree verification."""
+    total_q, h_q, d = q.shape
+    p, h_kv, ps, kd = k_pool.shape
+    _need(d == kd, "prefill: head_dim mismatch Q vs K pool")
+    _need(h_q % h_kv == 0, "prefill: H_q must be divisible by H_kv")
+    _need(d <= 256, f"prefill: head_dim {d} > D_MAX 256")
+    _need(d % 32 == 0, f"prefill: head_dim {d} must be a multiple of 32")
+    n_blk, max_blocks = block_table.shape
+    _need(cu_seqlens.shape[0] == n_blk + 1 and seq_id_per_q.shape[0] == total_q and kv_offsets.shape[0] == n_blk,
+          f"prefill: shape mismatch (block_table N={n_blk}, cu_seqlens={cu_seqlens.shape[0]}, "
+          f"seq_id_per_q={seq_id_per_q.shape[0]}, kv_offsets={kv_offsets.shape[0]})")
+    _need(k_pool.dtype == q.dtype and v_pool.dtype == q.dtype, "prefill: Q/K/V dtype mismatch")
+    _contig("prefill", q=q, k_pool=k_pool, v_pool=v_pool, block_table=block_table, cu_seqlens=cu_seqlens,
+            seq_id_per_q=seq_id_per_q, kv_offsets=kv_offsets)
+    out = torch.zeros_like(q)
+    check(lib.vx_paged_attention(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_table.data_ptr(),
+                                 cu_seqlens.data_ptr(), seq_id_per_q.data_ptr(), kv_offsets.data_ptr(),
+                                 _p(tree_mask), out.data_ptr(), total_q, n_blk, max_blocks, p, h_q, h_kv, d,
+                                 ps, scale, sliding_window, _dt(q, "prefill"), _stream()))
+    return out
+
+
+def paged_decode_attention(q, k_pool, v_pool, block_table, kv_lens, scale, sliding_window=0):
+    """paged_decode_attention (metal_kernels.rs:1227-1235)."""
+    n, h_q, d = q.shape
+    p, h_kv, ps, kd = k_pool.shape
+    _need(k_pool.shape == v_pool.shape and d == kd,
+          "paged_decode_attention: K/V pool shapes must match Q head_dim")
+    _need(h_q % h_kv == 0, f"paged_decode_attention: H_q={h_q} must be divisible by H_kv={h_kv}")
+    _need(d <= 256, f"paged_decode_attention: head_dim {d} > D_MAX 256")
+    _need(d % 32 == 0, f"paged_decode_attention: head_dim {d} not divisible by 32")
+    n_bt, max_blocks = block_table.shape
+    _need(n_bt == n, f"paged_decode_attention: block_table N={n_bt} mismatches Q N={n}")
+    _need(kv_lens.shape[0] == n, f"paged_decode_attention: kv_lens N={kv_lens.shape[0]} mismatches Q N={n}")
+    out = torch.zeros_like(q)
+    check(lib.vx_paged_decode_attention(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                                        block_table.data_ptr(), kv_lens.data_ptr(), out.data_ptr(), n,
+                                        max_blocks, p, h_q, h_kv, d, ps, scale, sliding_window,
+                                        _dt(q, "paged_decode_attention"), _stream()))
+    return out
+
+
+def batched_rope_decode(x, cos, sin, offsets):
+    """batched_rope_decode (metal_kernels.rs:1414-1419): in place on x [N, H, D]."""
+    n, h, d = x.shape
+    lmax, half = cos.shape
+    _need(tuple(sin.shape) == (lmax, half) and half * 2 == d,
+          f"batched_rope_decode: cos/sin shape [Lmax, {half}] mismatches D={d}")
+    _need(offsets.shape[0] == n, f"batched_rope_decode: offsets N={offsets.shape[0]} mismatches X N={n}")
+    _need(cos.dtype == x.dtype and sin.dtype == x.dtype, "batched_rope_decode: cos/sin dtype must match X")
+    _contig("batched_rope_decode", x=x, cos=cos, sin=sin, offsets=offsets)
+    check(lib.vx_rope_inplace(x.data_ptr(), cos.data_ptr(), sin.data_ptr(), offsets.data_ptr(), n, h, d, lmax,
+                              _dt(x, "batched_rope_decode"), _stream()))
+
+
+def batched_scatter(pool, values, page_ids, slots):
+    """batched_scatter (metal_kernels.rs:1543-1548): pool[page_ids[n], h, slots[n], :] = values[n]."""
+    p, h, s, d = pool.shape
+    n, vh, vd = values.shape
+    _need(vh == h and vd == d, f"batched_scatter: values [{n},{vh},{vd}] mismatches pool [_,{h},_,{d}]")
+    _need(page_ids.shape[0] == n and slots.shape[0] == n, "batched_scatter: page_ids/slots N mismatches values N")
+    _need(pool.dtype == values.dtype, "batched_scatter: pool/values dtype mismatch")
+    _contig("batched_scatter", pool=pool, values=values, page_ids=page_ids, slots=slots)
+    check(lib.vx_kv_scatter(pool.data_ptr(), values.data_ptr(), page_ids.data_ptr(), slots.data_ptr(), n, p, h,
+                            s, d, _dt(pool, "batched_scatter"), _stream()))
+
+
+# ------------------------------------------------------------------ acceptance
+def argmax_rows(logits):
+    rows, vocab = logits.shape
+    out = torch.zeros(rows, dtype=torch.int32, device=logits.device)
+    check(lib.vx_argmax_rows(logits.data_ptr(), out.data_ptr(), rows, vocab, _dt(logits, "argmax"), _stream()))
+    return out
+
+
+def accept_greedy(logits, candidates):
+    """logits [B, k+1, V]; candidates [B, k] -> (accepted [B], tokens [B, k+1])."""
+    b, r, v = logits.shape
+    acc = torch.zeros(b, dtype=torch.int32, device=logits.device)
+    tok = torch.zeros((b, r), dtype=torch.int32, device=logits.device)
+    check(lib.vx_accept_greedy(logits.data_ptr(), candidates.data_ptr(), acc.data_ptr(), tok.data_ptr(), b,
+                               r - 1, v, _dt(logits, "accept_greedy"), _stream()))
+    return acc, tok
+
+
+def accept_stochastic(target_logits, draft_logits, candidates, uniforms, temperature):
+    b, r, v = target_logits.shape
+    acc = torch.zeros(b, dtype=torch.int32, device=target_logits.device)
+    tok = torch.zeros((b, r), dtype=torch.int32, device=target_logits.device)
+    check(lib.vx_accept_stochastic(target_logits.data_ptr(), draft_logits.data_ptr(), candidates.data_ptr(),
+                                   uniforms.data_ptr(), acc.data_ptr(), tok.data_ptr(), b, r - 1, v,
+                                   temperature, _dt(target_logits, "accept_stochastic"), None, 0, _stream()))
+    return acc, tok
+
+
+def sample_rows(logits, uniforms, temperature, uniform_stride=1):
+    rows, v = logits.shape
+    out = torch.zeros(rows, dtype=torch.int32, device=logits.device)
+    check(lib.vx_sample_rows(logits.data_ptr(), uniforms.data_ptr(), uniform_stride, out.data_ptr(), rows, v,
+                             temperature, _dt(logits, "sample"), None, 0, _stream()))
+    return out
+
+
+def accept_tree(logits, parents, node_tokens):
+    """logits [B, R, V]; parents: host ints (parents[0] = -1); node_tokens [B, R]."""
+    import ctypes as C
+
+    b, r, v = logits.shape
+    par = (C.c_int32 * r)(*[int(x) for x in parents])
+    acc = torch.zeros(b, dtype=torch.int32, device=logits.device)
+    path = torch.zeros((b, r), dtype=torch.int32, device=logits.device)
+    tok = torch.zeros((b, r), dtype=torch.int32, device=logits.device)
+    check(lib.vx_accept_tree(logits.data_ptr(), C.cast(par, C.c_void_p), node_tokens.data_ptr(), acc.data_ptr(),
+                             path.data_ptr(), tok.data_ptr(), b, r, v, _dt(logits, "accept_tree"), _stream()))
+    return acc, path, tok
