@@ -54,7 +54,8 @@ typedef enum {
 /* Extended int4 GEMM: X is f16 (any value representable in f16, optionally
  * holding X_true * 2^-x_shift), scales/biases f16 [N, K/g], accumulation in
  * f32, result rounded to `round_dtype` semantics and stored as `y_dtype`.
- * workspace (device, >= vx_qmm_workspace_size bytes, first 64 KiB zeroed
+ * Requires group_size 64, K % 128 == 0, X 16-byte aligned, qweight rows
+ * 16-byte aligned, scales/biases 4-byte aligned.  workspace (device, >= vx_qmm_workspace_size bytes, first 64 KiB zeroed
  * once by the caller and left zero by the kernel) may be NULL to use the
  * per-stream library workspace. */
 int vx_qmm_4bit_ex(const void *x, const uint32_t *qweight, const void *scales,
@@ -62,6 +63,20 @@ int vx_qmm_4bit_ex(const void *x, const uint32_t *qweight, const void *scales,
                    int64_t k, int64_t group_size, int x_shift, int round_dtype, int y_dtype,
                    int epilogue, void *workspace, size_t workspace_bytes, void *stream);
 size_t vx_qmm_workspace_size(int64_t m, int64_t n, int64_t k);
+
+/* Packed weights for the verify path (no reference counterpart: the
+ * reference's Metal kernel reads MLX's row-major words, metal_kernels.rs
+ * :418-479; the packed form holds the same values).  Per 16-row tile and
+ * 128-wide k step, one 1152-byte block: 1024 bytes of nibbles in MFMA lane
+ * order, then 32 (scale, bias) f16 pairs.  N % 16 == 0, K % 128 == 0, group
+ * size 64.  vx_qmm_pack_4bit converts device MLX tensors on `stream`;
+ * vx_qmm_4bit_packed is vx_qmm_4bit_ex over packed weights. */
+size_t vx_qmm_packed_size(int64_t n, int64_t k);
+int vx_qmm_pack_4bit(const uint32_t *qweight, const void *scales, const void *biases, void *packed,
+                     int64_t n, int64_t k, void *stream);
+int vx_qmm_4bit_packed(const void *x, const void *packed, void *y, const void *residual, int64_t m,
+                       int64_t n, int64_t k, int x_shift, int round_dtype, int y_dtype, int epilogue,
+                       void *workspace, size_t workspace_bytes, void *stream);
 
 /* Replaces paged_prefill_attention (metal_kernels.rs:1680-1690; validation
  * :1697-1745; kernel MSL :307-395) and, with tree_mask, extends it to tree

@@ -2,6 +2,7 @@
 include/velox_hip.h, and rejects invalid arguments with the reference's
 messages before touching a device (no compute calls here)."""
 import ctypes as C
+import os
 
 import pytest
 
@@ -14,6 +15,18 @@ def test_every_declared_symbol_is_exported():
     missing = [s for s in syms if not hasattr(_lib.lib, s)]
     assert not missing, missing
     assert _lib.lib.vx_version().decode().startswith("velox_amd")
+
+
+def test_one_hip_runtime_whatever_the_import_order():
+    """Importing velox_amd before torch must not load a second HIP runtime."""
+    import subprocess
+    import sys
+
+    code = ("import velox_amd, torch; m = open('/proc/self/maps').read(); "
+            "print(len({l.split()[-1] for l in m.splitlines() if 'amdhip64' in l}))")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True,
+                         cwd=os.path.dirname(_lib.HERE))
+    assert out.stdout.strip() == "1", out.stdout + out.stderr
 
 
 def _err(rc):

@@ -157,6 +157,61 @@ def test_qmm_epilogues(cuda):
     assert (d <= bound).all(), f"residual: {int((d > bound).sum())} elements beyond the propagated bound"
 
 
+def unpack_blocks(packed, n, k):
+    """Decode the packed layout (1152-byte blocks per 16-row tile and 128-wide
+    k step: 64 lanes x 16 bytes of words whose nibbles of k0..k7 sit at
+    positions 0,4,1,5,2,6,3,7, then 32 (scale, bias) f16 pairs) back to MLX
+    tensors, independently of the GEMM kernels."""
+    blk = packed.reshape(n // 16, k // 128, 1152)
+    words = blk[:, :, :1024].copy().view(np.uint32).reshape(n // 16, k // 128, 4, 16, 4)  # tile, step, kq, row, word
+    pos = [0, 4, 1, 5, 2, 6, 3, 7]  # nibble position of k
+    natural = np.zeros_like(words)
+    for kk, p in enumerate(pos):
+        natural |= ((words >> np.uint32(4 * p)) & np.uint32(0xF)) << np.uint32(4 * kk)
+    qw = natural.transpose(0, 3, 1, 2, 4).reshape(n, k // 8)
+    sb = blk[:, :, 1024:].copy().view(np.uint16).reshape(n // 16, k // 128, 16, 2, 2)  # tile, step, row, half, (s,b)
+    sb = sb.transpose(0, 2, 1, 3, 4).reshape(n, k // 64, 2)
+    return qw, sb[..., 0], sb[..., 1]
+
+
+@pytest.mark.parametrize("shape", [(64, 256), (4608, 2560), (2560, 9728)], ids=lambda s: f"n{s[0]}k{s[1]}")
+def test_qmm_pack_layout_round_trip(cuda, shape):
+    """The packed blocks hold exactly the MLX words and f16 affine params."""
+    from velox_amd import ops
+
+    n, k = shape
+    lin = synth_linear(n, k, 11)
+    packed = ops.qmm_pack_4bit(u32(lin["qweight"]), dev(lin["scales"]), dev(lin["biases"]))
+    qw, sc, bi = unpack_blocks(packed.cpu().numpy(), n, k)
+    assert np.array_equal(qw, lin["qweight"].view(np.uint32))
+    assert np.array_equal(sc, lin["scales"].view(np.uint16))
+    assert np.array_equal(bi, lin["biases"].view(np.uint16))
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 33, 80, 97])
+@pytest.mark.parametrize("epi", ["store", "residual", "swiglu"])
+def test_qmm_packed_equals_row_major(cuda, m, epi):
+    """The packed-weight GEMM runs the same arithmetic in the same order as the
+    row-major f16 path, so the two agree bit for bit; the row-major path is
+    pinned to the oracle by the config-1 and epilogue tests."""
+    from velox_amd import _lib, ops
+
+    n, k = (2048, 2560) if epi != "residual" else (2560, 4096)
+    lin = synth_linear(n, k, 12)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float16)
+    W, S, B = u32(lin["qweight"]), dev(lin["scales"]), dev(lin["biases"])
+    packed = ops.qmm_pack_4bit(W, S, B)
+    e = {"store": _lib.EPI_STORE, "residual": _lib.EPI_RESIDUAL, "swiglu": _lib.EPI_SWIGLU}[epi]
+    cols = n // 2 if epi == "swiglu" else n
+    r = torch.from_numpy(np.random.default_rng(m + 1).standard_normal((m, cols)).astype(np.float32)).to(
+        torch.bfloat16).cuda()
+    a = r.clone()
+    b = r.clone()
+    ops.qmm_4bit_ex(dev(x), W, S, B, a, residual=a if epi == "residual" else None, epilogue=e)
+    ops.qmm_4bit_packed(dev(x), packed, n, b, residual=b if epi == "residual" else None, epilogue=e)
+    assert torch.equal(a, b)
+
+
 def test_qmm_validation_errors(cuda):
     from velox_amd import ops
     from velox_amd._lib import VeloxError

@@ -20,6 +20,26 @@ if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is missing: build it with `python velox_amd/build.py` "
                       "(velox_amd has no CPU fallback)")
 
+
+
+def _share_torch_hip_runtime() -> None:
+    """Bind the library to the HIP runtime PyTorch ships, when PyTorch is
+    installed.  libtorch_hip needs `libamdhip64.so` from its own lib folder,
+    this library `libamdhip64.so.7`; loaded in the other order the process
+    would hold two HIP (and HSA) runtimes, and the second one to initialise
+    finds no device.  Preloading torch's copy (soname libamdhip64.so.7) makes
+    both names resolve to it."""
+    import importlib.util
+
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return
+    rt = os.path.join(list(spec.submodule_search_locations)[0], "lib", "libamdhip64.so")
+    if os.path.exists(rt):
+        C.CDLL(rt, mode=C.RTLD_GLOBAL)
+
+
+_share_torch_hip_runtime()
 lib = C.CDLL(LIB_PATH)
 
 vp = C.c_void_p
@@ -71,6 +91,9 @@ _SIGS = {
     "vx_qmm_4bit_ex": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i32, i32, i32, i32, vp,
                              C.c_size_t, vp]),
     "vx_qmm_workspace_size": (C.c_size_t, [i64, i64, i64]),
+    "vx_qmm_packed_size": (C.c_size_t, [i64, i64]),
+    "vx_qmm_pack_4bit": (i32, [vp, vp, vp, vp, i64, i64, vp]),
+    "vx_qmm_4bit_packed": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, i32, i32, i32, vp, C.c_size_t, vp]),
     "vx_paged_attention": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
                                  i64, i64, f32, C.c_uint32, i32, vp]),
     "vx_paged_decode_attention": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64,

@@ -88,12 +88,11 @@ int stream_workspace(hipStream_t s, size_t bytes, void **out) {
 }
 
 // kernels in the other translation units
-int qmm_fast(const void *x, const uint32_t *w, const void *s, const void *b, void *y, const void *resid,
-             int64_t M, int64_t N, int64_t K, int x_dt, int x_shift, int round_dt, int y_dt, int epi,
-             void *workspace, size_t ws_bytes, hipStream_t st);
-int qmm_fast_scaled(const void *x, const uint32_t *w, const void *s, const void *b, void *y,
-                    const void *resid, int64_t M, int64_t N, int64_t K, int x_shift, int y_shift,
-                    int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes, hipStream_t st);
+size_t qmm_packed_bytes(int64_t n, int64_t k);
+int qmm_pack(const uint32_t *w, const void *s, const void *b, void *out, int64_t N, int64_t K, hipStream_t st);
+int qmm_packed(const void *x, const void *packed, void *y, const void *resid, int64_t M, int64_t N, int64_t K,
+               int x_shift, int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
+               hipStream_t st);
 size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi);
 size_t attn_workspace_bytes(int64_t n_seqs, int64_t h_kv, int64_t n_qtiles, int64_t n_splits, int64_t D);
 int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool, const uint32_t *bt,
@@ -290,8 +289,7 @@ extern "C" void *vx_pages_pool(vx_pages *p, int64_t layer, int kv) {
 namespace {
 
 struct QLinDev {
-    uint32_t *w = nullptr;
-    uint16_t *s = nullptr, *b = nullptr;  // f16 carriers of the bf16 affine params
+    void *packed = nullptr;  // packed int4 blocks; affine params as f16 carriers of bf16 values
     int64_t n = 0, k = 0;
 };
 
@@ -443,10 +441,30 @@ int upload_qlin(vx_model *m, const std::vector<const vx_qlinear_host *> &parts,
     }
     out->n = n;
     out->k = k;
-    VX_TRY(dev_upload(m, w.data(), w.size() * 4, (void **)&out->w));
-    VX_TRY(dev_upload(m, s.data(), s.size() * 2, (void **)&out->s));
-    VX_TRY(dev_upload(m, b.data(), b.size() * 2, (void **)&out->b));
-    return 0;
+    // stage the row-major tensors, pack on the device, drop the staging copies
+    void *tw = nullptr, *ts = nullptr, *tb = nullptr, *pk = nullptr;
+    auto release = [&]() {
+        (void)hipFree(tw);
+        (void)hipFree(ts);
+        (void)hipFree(tb);
+    };
+    if (hipMalloc(&tw, w.size() * 4) != hipSuccess || hipMalloc(&ts, s.size() * 2) != hipSuccess ||
+        hipMalloc(&tb, b.size() * 2) != hipSuccess || hipMalloc(&pk, qmm_packed_bytes(n, k)) != hipSuccess) {
+        release();
+        (void)hipFree(pk);
+        return set_error("model: out of device memory for weights");
+    }
+    m->allocs.push_back(pk);
+    int rc = 0;
+    if (hipMemcpy(tw, w.data(), w.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ts, s.data(), s.size() * 2, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(tb, b.data(), b.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+        rc = set_error("model: weight upload failed");
+    if (!rc) rc = qmm_pack((const uint32_t *)tw, ts, tb, pk, n, k, nullptr);
+    if (!rc && hipDeviceSynchronize() != hipSuccess) rc = set_error("model: weight packing failed");
+    release();
+    out->packed = pk;
+    return rc;
 }
 
 int upload_bf16(vx_model *m, const uint16_t *f16, int64_t n, uint16_t **out) {
@@ -467,6 +485,7 @@ extern "C" int vx_model_create(const vx_qwen3_config *cfg, const vx_weights_host
     VX_REQUIRE(HK > 0 && HQ % HK == 0, "model: n_heads must be divisible by n_kv_heads");
     VX_REQUIRE(D % 32 == 0 && D <= 256, "model: head_dim must be a multiple of 32 and <= 256");
     VX_REQUIRE(F % 16 == 0, "model: intermediate size must be a multiple of 16");
+    VX_REQUIRE(cfg->vocab % 16 == 0, "model: vocab must be a multiple of 16");
     auto m = std::make_unique<vx_model>();
     m->cfg = *cfg;
     m->L = L;
@@ -680,7 +699,7 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, QW + 2 * KW, H, false));
-            VX_TRY(qmm_fast_scaled(xn, ly.qkv.w, ly.qkv.s, ly.qkv.b, qkv, nullptr, R, QW + 2 * KW, H, 0, 0, VX_BF16,
+            VX_TRY(qmm_packed(xn, ly.qkv.packed, qkv, nullptr, R, QW + 2 * KW, H, 0, 0, VX_BF16,
                                    VX_BF16, VX_EPI_STORE, ws, ws_bytes, st));
         }
         {
@@ -696,7 +715,7 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, H, QW, true));
-            VX_TRY(qmm_fast_scaled(attn, ly.o.w, ly.o.s, ly.o.b, h, h, R, H, QW, 0, 0, VX_BF16, VX_BF16,
+            VX_TRY(qmm_packed(attn, ly.o.packed, h, h, R, H, QW, 0, 0, VX_BF16, VX_BF16,
                                    VX_EPI_RESIDUAL, ws, ws_bytes, st));
         }
         {
@@ -705,12 +724,12 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, 2 * F, H, false) - 2.0 * R * F);
-            VX_TRY(qmm_fast_scaled(xn, ly.gu.w, ly.gu.s, ly.gu.b, act, nullptr, R, 2 * F, H, 0, kMlpShift, VX_BF16,
+            VX_TRY(qmm_packed(xn, ly.gu.packed, act, nullptr, R, 2 * F, H, 0, kMlpShift, VX_BF16,
                                    VX_F16, VX_EPI_SWIGLU, ws, ws_bytes, st));
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, H, F, true));
-            VX_TRY(qmm_fast_scaled(act, ly.down.w, ly.down.s, ly.down.b, h, h, R, H, F, kMlpShift, 0, VX_BF16,
+            VX_TRY(qmm_packed(act, ly.down.packed, h, h, R, H, F, kMlpShift, 0, VX_BF16,
                                    VX_BF16, VX_EPI_RESIDUAL, ws, ws_bytes, st));
         }
     }
@@ -721,7 +740,7 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     }
     {
         ProfScope ps_(prof, st, PC_QMM, qmm_bytes(lrows, c.vocab, H, false));
-        VX_TRY(qmm_fast_scaled(xn, m->lm.w, m->lm.s, m->lm.b, logits, nullptr, lrows, c.vocab, H, 0, 0, VX_BF16,
+        VX_TRY(qmm_packed(xn, m->lm.packed, logits, nullptr, lrows, c.vocab, H, 0, 0, VX_BF16,
                                VX_BF16, VX_EPI_STORE, ws, ws_bytes, st));
     }
     return 0;

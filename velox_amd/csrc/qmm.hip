@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "vx_common.h"
 
@@ -43,6 +44,13 @@ constexpr int kWaves = 4;
 constexpr int kChunkGroups = 4;          // groups of 64 staged per LDS chunk
 constexpr size_t kCounterBytes = 65536;  // reserved head of the workspace (kept zero)
 constexpr size_t kMaxPartialBytes = (size_t)96 << 20;
+// Packed weight layout of the streaming kernel: per 16-row tile and 128-wide
+// k step one block of 1024 bytes of nibbles in MFMA lane order (lane L: row
+// L%16 of the tile, k 32*(L/16) .. +31 of the step, four words; inside a word
+// the nibbles of k0..k7 sit at positions 0,4,1,5,2,6,3,7) followed
+// by 32 (scale, bias) f16 pairs (row r, group half h at index 2r + h).  Tiles
+// are contiguous over their steps, so a wave streams contiguous memory.
+constexpr int kPackBlock = 1152;
 
 struct QmmArgs {
     const void *x;
@@ -54,6 +62,7 @@ struct QmmArgs {
     float *partial;
     int M, N, K, G;
     int splits, gps;
+    int S, sps;  // streaming kernel: 128-wide k steps, steps per split
     int col_blocks, m_blocks, per_xcd, total_items;
     int epi, round_dt, y_dt;
     float acc_scale;    // 2^x_shift
@@ -86,6 +95,44 @@ __device__ __forceinline__ half8_t dequant_f16(uint32_t word, half2_t s2, half2_
         r[2 * j + 1] = w[1];
     }
     return r;
+}
+
+// v_and_or_b32 with both constants in VGPRs (CDNA3 VOP3 takes no literal,
+// so the compiler otherwise splits it into v_and + v_or).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(mask), "v"(bits));
+    return r;
+}
+
+// Constants of dequant8, kept in VGPRs by the caller.
+struct DqConst {
+    uint32_t m_lo, m_hi, magic_lo, magic_hi;
+    half2_t off_lo, off_hi;
+};
+__device__ __forceinline__ DqConst dq_const() {
+    DqConst c;
+    c.m_lo = 0x000F000Fu;
+    c.m_hi = 0x00F000F0u;
+    c.magic_lo = 0x64006400u;  // f16 1024: nibble at mantissa bits 0-3 reads as 1024 + q
+    c.magic_hi = 0x54005400u;  // f16 64: nibble at mantissa bits 4-7 reads as 64 + q
+    c.off_lo = (half2_t){(vx_half)1024.0f, (vx_half)1024.0f};
+    c.off_hi = (half2_t){(vx_half)64.0f, (vx_half)64.0f};
+    return c;
+}
+
+// Eight nibbles of one word -> eight f16 weights fma(q, s, b) (one rounding),
+// in the order (n0, n4, n1, n5, n2, n6, n3, n7): pairs (n_j, n_j+4) share a
+// register.  Nibbles at bits 0-3 / 4-7 of each half are read in place with
+// exponent 1024 / 64; the upper byte pair after one shift: 13 VALU per word.
+__device__ __forceinline__ half8_t dequant8(uint32_t word, half2_t s2, half2_t b2, const DqConst &c) {
+    const uint32_t w8 = word >> 8;
+    const half2_t p0 = __builtin_bit_cast(half2_t, and_or(word, c.m_lo, c.magic_lo)) - c.off_lo;
+    const half2_t p1 = __builtin_bit_cast(half2_t, and_or(word, c.m_hi, c.magic_hi)) - c.off_hi;
+    const half2_t p2 = __builtin_bit_cast(half2_t, and_or(w8, c.m_lo, c.magic_lo)) - c.off_lo;
+    const half2_t p3 = __builtin_bit_cast(half2_t, and_or(w8, c.m_hi, c.magic_hi)) - c.off_hi;
+    const half2_t w0 = p0 * s2 + b2, w1 = p1 * s2 + b2, w2 = p2 * s2 + b2, w3 = p3 * s2 + b2;
+    return (half8_t){w0[0], w0[1], w1[0], w1[1], w2[0], w2[1], w3[0], w3[1]};
 }
 
 __device__ __forceinline__ bf16x8_t codes_bf16(uint32_t word) {
@@ -136,133 +183,12 @@ __device__ __forceinline__ void epi_swiglu(const QmmArgs &a, int row, int f, flo
     store_dt(a.y, (int64_t)row * (a.N / 2) + f, v * a.store_scale, a.y_dt);
 }
 
-template <int MT, int NT, bool XBF>
-__global__ __launch_bounds__(256) void qmm_int4_kernel(QmmArgs a) {
-    __shared__ uint4 xs[kChunkGroups * 2 * MT * 64];
-    __shared__ float xsum[XBF ? kChunkGroups * MT * 16 : 1];
-
-    const int bid = blockIdx.x;
-    const int item = (bid & 7) * a.per_xcd + (bid >> 3);
-    if (item >= a.total_items) return;
-    const int cb = item / a.splits;
-    const int sp = item - cb * a.splits;
-    const int mb = blockIdx.y;
-    const int m0 = mb * MT * 16;
-    const int g_lo = sp * a.gps;
-    const int g_hi = min(a.G, g_lo + a.gps);
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int kq = lane >> 4;
-    const int col0 = cb * (kWaves * NT * 16) + wave * NT * 16 + (lane & 15);
-    const int64_t kw = a.K / 8;
-
-    floatx4 acc[MT][NT];
-#pragma unroll
-    for (int t = 0; t < MT; t++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[t][nt] = (floatx4){0.f, 0.f, 0.f, 0.f};
-
-    const uint16_t *xh = (const uint16_t *)a.x;
-    for (int gc = g_lo; gc < g_hi; gc += kChunkGroups) {
-        const int ng = min(kChunkGroups, g_hi - gc);
-        // ---- weights + affine params for this chunk (issued before the barrier)
-        uint2 wv[kChunkGroups][NT];
-        uint2 sv[NT], bv[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int col = min(col0 + nt * 16, a.N - 1);
-            const uint32_t *wr = a.w + (int64_t)col * kw + (int64_t)gc * 8 + 2 * kq;
-#pragma unroll
-            for (int gg = 0; gg < kChunkGroups; gg++)
-                wv[gg][nt] = gg < ng ? *(const uint2 *)(wr + gg * 8) : make_uint2(0u, 0u);
-            sv[nt] = *(const uint2 *)(a.s + (int64_t)col * a.G + gc);
-            bv[nt] = *(const uint2 *)(a.b + (int64_t)col * a.G + gc);
-        }
-        __syncthreads();  // previous chunk's fragments fully consumed
-        // ---- stage activations in fragment order
-        for (int u = tid; u < ng * 2 * MT * 64; u += 256) {
-            const int l = u & 63;
-            int r = u >> 6;
-            const int t = r % MT;
-            r /= MT;
-            const int s = r & 1;
-            const int gg = r >> 1;
-            const int row = m0 + t * 16 + (l & 15);
-            const int kk = (gc + gg) * 64 + 8 * (2 * (l >> 4) + s);
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (row < a.M) v = *(const uint4 *)(xh + (int64_t)row * a.K + kk);
-            xs[u] = permute_k8(v);
-        }
-        if (XBF) {
-            for (int idx = tid; idx < ng * MT * 16; idx += 256) {
-                const int gg = idx / (MT * 16);
-                const int rr = idx - gg * MT * 16;
-                const int row = m0 + rr;
-                float sum = 0.f;
-                if (row < a.M) {
-                    const uint16_t *xr = xh + (int64_t)row * a.K + (gc + gg) * 64;
-                    for (int e = 0; e < 64; e++) sum += bf16_bits_to_f32(xr[e]);
-                }
-                xsum[gg * MT * 16 + rr] = sum;
-            }
-        }
-        __syncthreads();
-        // ---- MFMA over the chunk
-#pragma unroll
-        for (int gg = 0; gg < kChunkGroups; gg++) {
-            if (gg >= ng) break;
-            if constexpr (!XBF) {
-#pragma unroll
-                for (int s = 0; s < 2; s++) {
-                    half8_t af[MT];
-#pragma unroll
-                    for (int t = 0; t < MT; t++)
-                        af[t] = __builtin_bit_cast(half8_t, xs[((gg * 2 + s) * MT + t) * 64 + lane]);
-#pragma unroll
-                    for (int nt = 0; nt < NT; nt++) {
-                        const uint32_t word = s == 0 ? wv[gg][nt].x : wv[gg][nt].y;
-                        const uint32_t sbits = gg < 2 ? sv[nt].x : sv[nt].y;
-                        const uint32_t bbits = gg < 2 ? bv[nt].x : bv[nt].y;
-                        const uint16_t sh = (gg & 1) ? (uint16_t)(sbits >> 16) : (uint16_t)sbits;
-                        const uint16_t bh = (gg & 1) ? (uint16_t)(bbits >> 16) : (uint16_t)bbits;
-                        const vx_half sc = __builtin_bit_cast(vx_half, sh);
-                        const vx_half bi = __builtin_bit_cast(vx_half, bh);
-                        const half8_t bf = dequant_f16(word, (half2_t){sc, sc}, (half2_t){bi, bi});
-#pragma unroll
-                        for (int t = 0; t < MT; t++)
-                            acc[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf, acc[t][nt], 0, 0, 0);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    const uint32_t sbits = gg < 2 ? sv[nt].x : sv[nt].y;
-                    const uint32_t bbits = gg < 2 ? bv[nt].x : bv[nt].y;
-                    const float sc = bf16_bits_to_f32((gg & 1) ? (uint16_t)(sbits >> 16) : (uint16_t)sbits);
-                    const float bi = bf16_bits_to_f32((gg & 1) ? (uint16_t)(bbits >> 16) : (uint16_t)bbits);
-                    const float boff = bi - 128.0f * sc;
-                    const bf16x8_t b0 = codes_bf16(wv[gg][nt].x);
-                    const bf16x8_t b1 = codes_bf16(wv[gg][nt].y);
-#pragma unroll
-                    for (int t = 0; t < MT; t++) {
-                        floatx4 tmp = {0.f, 0.f, 0.f, 0.f};
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8_t, xs[((gg * 2 + 0) * MT + t) * 64 + lane]), b0, tmp, 0, 0, 0);
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8_t, xs[((gg * 2 + 1) * MT + t) * 64 + lane]), b1, tmp, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const float xsr = xsum[gg * MT * 16 + t * 16 + 4 * kq + r];
-                            acc[t][nt][r] += sc * tmp[r] + boff * xsr;
-                        }
-                    }
-                }
-            }
-        }
-    }
-
-    // ---- split-K: publish the partial tile; qmm_reduce_kernel finishes
+// Writes a wave's accumulators: the split-K partial tile when the K range is
+// split (qmm_reduce_kernel finishes), else the epilogue.  C fragment layout of
+// v_mfma_f32_16x16x32: lane holds column lane%16, rows 4*(lane/16) + r.
+template <int MT, int NT>
+__device__ __forceinline__ void store_acc(const QmmArgs &a, const floatx4 (&acc)[MT][NT], int m0, int col0,
+                                          int sp, int kq) {
     if (a.splits > 1) {
 #pragma unroll
         for (int t = 0; t < MT; t++)
@@ -278,16 +204,14 @@ __global__ __launch_bounds__(256) void qmm_int4_kernel(QmmArgs a) {
             }
         return;
     }
-
-    // ---- epilogue
     if (a.epi == VX_EPI_SWIGLU) {
         // tiles come in (gate, up) pairs: global tile 2f = gate rows, 2f+1 = up rows
 #pragma unroll
         for (int t = 0; t < MT; t++)
 #pragma unroll
             for (int nt = 0; nt + 1 < NT; nt += 2) {
-                const int gtile = (col0 - (lane & 15)) / 16 + nt;
-                const int f = (gtile / 2) * 16 + (lane & 15);
+                const int gtile = (col0 - (col0 & 15)) / 16 + nt;
+                const int f = (gtile / 2) * 16 + (col0 & 15);
                 if (col0 + nt * 16 >= a.N) continue;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
@@ -309,6 +233,378 @@ __global__ __launch_bounds__(256) void qmm_int4_kernel(QmmArgs a) {
                 if (row < a.M) epi_elem(a, row, col, acc[t][nt][r]);
             }
         }
+}
+
+template <int MT, int NT, bool XBF>
+__global__ __launch_bounds__(256) void qmm_int4_kernel(QmmArgs a) {
+    // X tile of one chunk (4 groups x 64 k) in MFMA fragment order, double buffered
+    constexpr int UNITS = kChunkGroups * 2 * MT * 64;  // 16-byte fragments per chunk
+    constexpr int UPT = UNITS / 256;                   // per thread (= 2 * MT)
+    __shared__ uint4 xs[2][UNITS];
+    __shared__ float xsum[XBF ? 2 : 1][XBF ? kChunkGroups * MT * 16 : 1];
+
+    const int bid = blockIdx.x;
+    const int item = (bid & 7) * a.per_xcd + (bid >> 3);
+    if (item >= a.total_items) return;
+    const int cb = item / a.splits;
+    const int sp = item - cb * a.splits;
+    const int m0 = blockIdx.y * MT * 16;
+    const int g_lo = sp * a.gps;
+    const int g_hi = min(a.G, g_lo + a.gps);  // g_lo, g_hi are multiples of 4
+    const int nchunks = (g_hi - g_lo) / kChunkGroups;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int kq = lane >> 4;
+    const int col0 = cb * (kWaves * NT * 16) + wave * NT * 16 + (lane & 15);
+    const int kw = a.K / 8;
+
+    // per-thread staging map: unit u = tid + 256 j -> (row, k offset within the chunk)
+    const uint16_t *xh = (const uint16_t *)a.x;
+    int xoff[UPT];
+    bool xok[UPT];
+#pragma unroll
+    for (int j = 0; j < UPT; j++) {
+        const int r = wave + 4 * j;
+        const int t = r % MT;
+        const int q = r / MT;
+        const int row = m0 + t * 16 + (lane & 15);
+        xok[j] = row < a.M;
+        xoff[j] = (xok[j] ? row : 0) * a.K + (q >> 1) * 64 + 8 * (2 * kq + (q & 1));
+    }
+    const uint32_t *wbase[NT];
+    const uint16_t *sbase[NT], *bbase[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int col = min(col0 + nt * 16, a.N - 1);
+        wbase[nt] = a.w + (int64_t)col * kw + 2 * kq;
+        sbase[nt] = a.s + (int64_t)col * a.G;
+        bbase[nt] = a.b + (int64_t)col * a.G;
+    }
+
+    floatx4 acc[MT][NT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[t][nt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+
+    uint2 wc[kChunkGroups][NT], sc[NT], bc[NT];  // current chunk weights / affine params
+    uint4 xr[UPT];                              // next chunk activations (registers)
+
+    auto load_w = [&](int g, uint2 (&w)[kChunkGroups][NT], uint2 (&sv)[NT], uint2 (&bv)[NT]) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+            for (int gg = 0; gg < kChunkGroups; gg++) w[gg][nt] = *(const uint2 *)(wbase[nt] + (g + gg) * 8);
+            sv[nt] = *(const uint2 *)(sbase[nt] + g);
+            bv[nt] = *(const uint2 *)(bbase[nt] + g);
+        }
+    };
+    auto load_x = [&](int g) {
+#pragma unroll
+        for (int j = 0; j < UPT; j++)
+            xr[j] = xok[j] ? *(const uint4 *)(xh + xoff[j] + g * 64) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto store_x = [&](int buf, int g) {
+#pragma unroll
+        for (int j = 0; j < UPT; j++) xs[buf][tid + 256 * j] = permute_k8(xr[j]);
+        if constexpr (XBF) {
+            for (int idx = tid; idx < kChunkGroups * MT * 16; idx += 256) {
+                const int gg = idx / (MT * 16);
+                const int rr = idx - gg * MT * 16;
+                float sum = 0.f;
+                if (m0 + rr < a.M) {
+                    const uint16_t *xrow = xh + (int64_t)(m0 + rr) * a.K + (g + gg) * 64;
+                    for (int e = 0; e < 64; e++) sum += bf16_bits_to_f32(xrow[e]);
+                }
+                xsum[buf][idx] = sum;
+            }
+        }
+    };
+
+    load_w(g_lo, wc, sc, bc);
+    load_x(g_lo);
+    store_x(0, g_lo);
+    __syncthreads();
+
+    for (int c = 0; c < nchunks; c++) {
+        const int buf = c & 1;
+        const bool more = c + 1 < nchunks;
+        const int gn = g_lo + (c + 1) * kChunkGroups;
+        uint2 wn[kChunkGroups][NT], sn[NT], bn[NT];
+        if (more) {
+            load_x(gn);
+            load_w(gn, wn, sn, bn);
+        }
+#pragma unroll
+        for (int gg = 0; gg < kChunkGroups; gg++) {
+            if constexpr (!XBF) {
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    half8_t af[MT];
+#pragma unroll
+                    for (int t = 0; t < MT; t++)
+                        af[t] = __builtin_bit_cast(half8_t, xs[buf][((gg * 2 + s) * MT + t) * 64 + lane]);
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        const uint32_t word = s == 0 ? wc[gg][nt].x : wc[gg][nt].y;
+                        const uint32_t sbits = gg < 2 ? sc[nt].x : sc[nt].y;
+                        const uint32_t bbits = gg < 2 ? bc[nt].x : bc[nt].y;
+                        const uint16_t sh = (gg & 1) ? (uint16_t)(sbits >> 16) : (uint16_t)sbits;
+                        const uint16_t bh = (gg & 1) ? (uint16_t)(bbits >> 16) : (uint16_t)bbits;
+                        const vx_half svh = __builtin_bit_cast(vx_half, sh);
+                        const vx_half bvh = __builtin_bit_cast(vx_half, bh);
+                        const half8_t bf = dequant_f16(word, (half2_t){svh, svh}, (half2_t){bvh, bvh});
+#pragma unroll
+                        for (int t = 0; t < MT; t++)
+                            acc[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf, acc[t][nt], 0, 0, 0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const uint32_t sbits = gg < 2 ? sc[nt].x : sc[nt].y;
+                    const uint32_t bbits = gg < 2 ? bc[nt].x : bc[nt].y;
+                    const float svf = bf16_bits_to_f32((gg & 1) ? (uint16_t)(sbits >> 16) : (uint16_t)sbits);
+                    const float bvf = bf16_bits_to_f32((gg & 1) ? (uint16_t)(bbits >> 16) : (uint16_t)bbits);
+                    const float boff = bvf - 128.0f * svf;
+                    const bf16x8_t b0 = codes_bf16(wc[gg][nt].x);
+                    const bf16x8_t b1 = codes_bf16(wc[gg][nt].y);
+#pragma unroll
+                    for (int t = 0; t < MT; t++) {
+                        floatx4 tmp = {0.f, 0.f, 0.f, 0.f};
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8_t, xs[buf][((gg * 2 + 0) * MT + t) * 64 + lane]), b0, tmp, 0, 0, 0);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8_t, xs[buf][((gg * 2 + 1) * MT + t) * 64 + lane]), b1, tmp, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float xsr = xsum[buf][gg * MT * 16 + t * 16 + 4 * kq + r];
+                            acc[t][nt][r] += svf * tmp[r] + boff * xsr;
+                        }
+                    }
+                }
+            }
+        }
+        if (more) {
+            store_x(buf ^ 1, gn);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+                for (int gg = 0; gg < kChunkGroups; gg++) wc[gg][nt] = wn[gg][nt];
+                sc[nt] = sn[nt];
+                bc[nt] = bn[nt];
+            }
+        }
+        __syncthreads();
+    }
+
+    store_acc<MT, NT>(a, acc, m0, col0, sp, kq);
+}
+
+// f16 streaming kernel (the verify path's GEMM).  K advances in steps of 128
+// (two groups).  In a step, lane L reads one 16-byte piece of weight row
+// col = L%16 (+16 nt): the 32 k values 32*(L/16) .. +31, four packed words.
+// MFMA j (j < 4) of the step takes word j from every lane, so its 32-wide k
+// set is {32*kq + 8j + e}; the activation fragments are staged in LDS with the
+// same k set per lane (16 contiguous bytes, then permute_k8), so the dot
+// product is unchanged.  A lane's group is 2*step + kq/2, so each lane
+// dequantises with its own scale/bias.
+// Software pipeline: the weights, scales and activations of step s+P are
+// requested before step s is computed, in a ring of P+1 register slots (the
+// step loop is unrolled by the ring size so every slot is a fixed register
+// set); the activations of step s+1 move to the other LDS buffer after the
+// MFMAs of step s, one barrier per step.
+template <int MT, int NT, int P, bool PACKED>
+__global__ __launch_bounds__(256) void qmm_f16_stream_kernel(QmmArgs a) {
+    constexpr int R = P + 1;
+    static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
+    constexpr int FR = 4 * MT;  // activation fragments (j, t) per step
+    constexpr int UPT = MT;     // 16-byte fragment pieces per thread per step (FR * 64 / 256)
+    __shared__ uint4 xs[2][FR * 64];
+
+    const int bid = blockIdx.x;
+    const int item = (bid & 7) * a.per_xcd + (bid >> 3);
+    if (item >= a.total_items) return;
+    const int cb = item / a.splits;
+    const int sp = item - cb * a.splits;
+    const int m0 = blockIdx.y * MT * 16;
+    const int s_lo = sp * a.sps;
+    const int s_hi = min(a.S, s_lo + a.sps);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int kq = lane >> 4;
+    const int col0 = cb * (kWaves * NT * 16) + wave * NT * 16 + (lane & 15);
+
+    // activation pieces: unit u = tid + 256 i is fragment (j, t) = divmod(u / 64, MT), lane u % 64;
+    // rows past M re-read row M-1 (finite values whose results are never stored)
+    const uint16_t *xh = (const uint16_t *)a.x;
+    int xoff[UPT];
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + 256 * i;
+        const int ln = u & 63;
+        const int jt = u >> 6;
+        const int j = jt / MT;
+        const int t = jt - j * MT;
+        const int row = min(m0 + t * 16 + (ln & 15), a.M - 1);
+        xoff[i] = row * a.K + 32 * (ln >> 4) + 8 * j;
+    }
+    // MLX layout: weight row col, words 16 st + 4 kq .. +3; scales/biases
+    // [N, G] (the pair of groups of step st is one 32-bit word).
+    // Packed layout: block (tile, st) of kPackBlock bytes, this lane's 16
+    // bytes at lane*16 and its (scale, bias) pair at 1024 + 4 (2 (lane%16) + kq/2).
+    const uint4 *wrow[NT];
+    const uint32_t *srow[NT], *brow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        if constexpr (PACKED) {
+            const int tile = min(col0 / 16 + nt, a.N / 16 - 1);
+            const uint8_t *blk = (const uint8_t *)a.w + (int64_t)tile * a.S * kPackBlock;
+            wrow[nt] = (const uint4 *)blk + lane;
+            srow[nt] = (const uint32_t *)(blk + 1024) + 2 * (lane & 15) + (kq >> 1);
+            brow[nt] = nullptr;
+        } else {
+            const int col = min(col0 + nt * 16, a.N - 1);
+            wrow[nt] = (const uint4 *)(a.w + (int64_t)col * (a.K / 8)) + kq;
+            srow[nt] = (const uint32_t *)(a.s + (int64_t)col * a.G);
+            brow[nt] = (const uint32_t *)(a.b + (int64_t)col * a.G);
+        }
+    }
+    // byte selectors replicating one 16-bit half of a word into both halves
+    const uint32_t hsel = (kq & 2) ? 0x03020302u : 0x01000100u;
+    constexpr uint32_t kLoHalf = 0x01000100u, kHiHalf = 0x03020302u;
+    const DqConst dq = dq_const();
+
+    floatx4 acc[MT][NT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[t][nt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+
+    uint4 wr[R][NT];
+    uint32_t sr[R][NT], br[R][NT];
+    uint4 xr[R][UPT];
+
+    auto issue = [&](int st, uint4 (&w)[NT], uint32_t (&sv)[NT], uint32_t (&bv)[NT], uint4 (&xv)[UPT]) {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) xv[i] = *(const uint4 *)(xh + xoff[i] + st * 128);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            if constexpr (PACKED) {
+                w[nt] = wrow[nt][st * (kPackBlock / 16)];
+                sv[nt] = srow[nt][st * (kPackBlock / 4)];
+                bv[nt] = 0u;
+            } else {
+                w[nt] = wrow[nt][st * 4];
+                sv[nt] = srow[nt][st];
+                bv[nt] = brow[nt][st];
+            }
+        }
+    };
+    // packed weights hold each word's nibbles in the order dequant8 emits
+    // them as k (natural order), so only the row-major path permutes X
+    auto stage = [&](int buf, const uint4 (&xv)[UPT]) {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) xs[buf][tid + 256 * i] = PACKED ? xv[i] : permute_k8(xv[i]);
+    };
+
+    // One step: request step st+P into its ring slot (clamped to the last
+    // step so every path issues the same loads and the compiler's wait
+    // counts stay exact), run the MFMAs of step st, stage the activations of
+    // step st+1.
+    auto step = [&](int st, auto slot_c) {
+        constexpr int I = decltype(slot_c)::value;
+        constexpr int NX = (I + P) % R;
+        issue(min(st + P, s_hi - 1), wr[NX], sr[NX], br[NX], xr[NX]);
+        // keep the prefetch at the head of the step: if the scheduler sinks it
+        // below the MFMAs, consuming an older slot waits for every load in flight
+        __builtin_amdgcn_sched_barrier(0);
+        const int buf = (st - s_lo) & 1;
+        half2_t s2[NT], b2[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            if constexpr (PACKED) {
+                s2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt], sr[I][nt], kLoHalf));
+                b2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt], sr[I][nt], kHiHalf));
+            } else {
+                s2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt], sr[I][nt], hsel));
+                b2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(br[I][nt], br[I][nt], hsel));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            half8_t af[MT];
+#pragma unroll
+            for (int t = 0; t < MT; t++) af[t] = __builtin_bit_cast(half8_t, xs[buf][(j * MT + t) * 64 + lane]);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint32_t word = j == 0 ? wr[I][nt].x : j == 1 ? wr[I][nt].y : j == 2 ? wr[I][nt].z : wr[I][nt].w;
+                const half8_t bf = dequant8(word, s2[nt], b2[nt], dq);
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    acc[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf, acc[t][nt], 0, 0, 0);
+            }
+        }
+        stage(buf ^ 1, xr[(I + 1) % R]);  // past the last step this stages a copy nobody reads
+        __syncthreads();
+    };
+
+#pragma unroll
+    for (int i = 0; i < P; i++) issue(min(s_lo + i, s_hi - 1), wr[i], sr[i], br[i], xr[i]);
+    stage(0, xr[0]);
+    __syncthreads();
+
+    int st = s_lo;
+    for (; st + R <= s_hi; st += R) {
+        step(st + 0, std::integral_constant<int, 0>{});
+        if constexpr (R > 1) step(st + 1, std::integral_constant<int, 1 % R>{});
+        if constexpr (R > 2) step(st + 2, std::integral_constant<int, 2 % R>{});
+        if constexpr (R > 3) step(st + 3, std::integral_constant<int, 3 % R>{});
+        if constexpr (R > 4) step(st + 4, std::integral_constant<int, 4 % R>{});
+        if constexpr (R > 5) step(st + 5, std::integral_constant<int, 5 % R>{});
+    }
+    // tail: fewer than R steps remain; slot of step st + i is i
+    if (st < s_hi) step(st, std::integral_constant<int, 0>{});
+    if constexpr (R > 2) if (st + 1 < s_hi) step(st + 1, std::integral_constant<int, 1 % R>{});
+    if constexpr (R > 3) if (st + 2 < s_hi) step(st + 2, std::integral_constant<int, 2 % R>{});
+    if constexpr (R > 4) if (st + 3 < s_hi) step(st + 3, std::integral_constant<int, 3 % R>{});
+    if constexpr (R > 5) if (st + 4 < s_hi) step(st + 4, std::integral_constant<int, 4 % R>{});
+    store_acc<MT, NT>(a, acc, m0, col0, sp, kq);
+}
+
+// Word with nibbles k0..k7 (k at bits 4k) -> nibble positions
+// (k0, k2, k4, k6, k1, k3, k5, k7), so dequant8's pairs (p, p+4) come out as
+// (k0, k1), (k2, k3), ...: natural k order.
+__device__ __forceinline__ uint32_t pack_nibbles(uint32_t w) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        o |= ((w >> (8 * j)) & 0xFu) << (4 * j);             // k 2j     -> position j
+        o |= ((w >> (8 * j + 4)) & 0xFu) << (4 * j + 16);   // k 2j + 1 -> position j + 4
+    }
+    return o;
+}
+
+// MLX [N, K/8] words + [N, K/64] scales/biases -> packed blocks.  One
+// workgroup of 64 threads per (tile, step) block.
+__global__ __launch_bounds__(64) void qmm_pack_kernel(const uint32_t *w, const uint16_t *s, const uint16_t *b,
+                                                      uint8_t *out, int N, int K) {
+    const int S = K / 128, G = K / 64;
+    const int64_t blk = blockIdx.x;
+    const int tile = (int)(blk / S), st = (int)(blk - (int64_t)tile * S);
+    const int lane = threadIdx.x;
+    uint8_t *o = out + blk * kPackBlock;
+    const int row = tile * 16 + (lane & 15);
+    const uint4 v = *(const uint4 *)(w + (int64_t)row * (K / 8) + st * 16 + 4 * (lane >> 4));
+    *(uint4 *)(o + lane * 16) = make_uint4(pack_nibbles(v.x), pack_nibbles(v.y), pack_nibbles(v.z), pack_nibbles(v.w));
+    if (lane < 32) {
+        const int r = tile * 16 + (lane >> 1);
+        const int g = 2 * st + (lane & 1);
+        const uint32_t pair = (uint32_t)s[(int64_t)r * G + g] | ((uint32_t)b[(int64_t)r * G + g] << 16);
+        *(uint32_t *)(o + 1024 + lane * 4) = pair;
+    }
 }
 
 // Split-K finish: sum the partials of each output in split order, then the
@@ -376,7 +672,8 @@ __global__ void add_bias_kernel(void *y, const void *bias, int64_t m, int64_t n)
 }
 
 struct Plan {
-    int MT, NT, splits, gps, col_blocks, m_blocks, per_xcd, total_items;
+    bool stream;  // f16 streaming kernel (else the LDS-chunked kernel)
+    int MT, NT, P, splits, gps, sps, col_blocks, m_blocks, per_xcd, total_items;
     size_t partial_bytes;
 };
 
@@ -385,52 +682,109 @@ int env_int(const char *name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-Plan make_plan(int64_t M, int64_t N, int64_t K, int epi) {
+// Prefetch depth of the streaming kernel by row-tile count: the register ring
+// holds P+1 steps of weights and activations.
+constexpr int stream_depth(int mt) { return mt == 1 ? 4 : (mt == 2 ? 3 : 2); }
+
+Plan make_plan(int64_t M, int64_t N, int64_t K, int epi, bool stream) {
     Plan p{};
+    p.stream = stream;
     const int64_t mrows = std::min<int64_t>(M, 80);
     p.MT = (int)std::max<int64_t>(1, vx_cdiv(mrows, 16));
     p.m_blocks = (int)vx_cdiv(M, p.MT * 16);
-    int nt = p.MT >= 3 ? 4 : (p.MT == 2 ? 2 : 1);
-    if (epi == VX_EPI_SWIGLU) nt = std::max(nt, 2);
-    const int G = (int)(K / 64);
     const int cus = device_cu_count();
     const int target = 2 * cus;
-    // prefer narrower column blocks when the grid would be too small
-    while (nt > (epi == VX_EPI_SWIGLU ? 2 : 1) &&
-           vx_cdiv(N, kWaves * nt * 16) * p.m_blocks * std::max(1, G / kChunkGroups) < target)
-        nt /= 2;
-    nt = env_int("VX_QMM_NT", nt);
-    p.NT = nt;
-    p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 16);
-    const int items = p.col_blocks * p.m_blocks;
-    int splits = std::max(1, target / std::max(1, items));
-    splits = std::min(splits, std::max(1, G / kChunkGroups));
-    splits = env_int("VX_QMM_SPLITS", splits);
-    splits = std::max(1, std::min(splits, G / kChunkGroups));
-    int gps = (int)vx_cdiv(G, splits);
-    gps = (int)vx_cdiv(gps, kChunkGroups) * kChunkGroups;
-    splits = (int)vx_cdiv(G, gps);
-    // bound the partial-sum workspace
-    while (splits > 1 && (size_t)splits * M * N * 4 > kMaxPartialBytes) {
-        gps += kChunkGroups;
+    if (stream) {
+        const int S = (int)(K / 128);
+        int nt = p.MT >= 3 ? 4 : 2;
+        if (epi == VX_EPI_SWIGLU) nt = std::max(nt, 2);
+        while (nt > (epi == VX_EPI_SWIGLU ? 2 : 1) && vx_cdiv(N, kWaves * nt * 16) * p.m_blocks * 4 < target)
+            nt /= 2;
+        nt = env_int("VX_QMM_NT", nt);
+        p.NT = nt;
+        p.P = stream_depth(p.MT);
+        p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 16);
+        const int items = p.col_blocks * p.m_blocks;
+        int splits = std::max(1, target / std::max(1, items));
+        splits = env_int("VX_QMM_SPLITS", splits);
+        splits = std::max(1, std::min(splits, S));
+        int sps = (int)vx_cdiv(S, splits);
+        splits = (int)vx_cdiv(S, sps);
+        while (splits > 1 && (size_t)splits * M * N * 4 > kMaxPartialBytes) {
+            sps++;
+            splits = (int)vx_cdiv(S, sps);
+        }
+        p.splits = splits;
+        p.sps = sps;
+        p.gps = 2 * sps;
+    } else {
+        int nt = p.MT >= 3 ? 4 : (p.MT == 2 ? 2 : 1);
+        if (epi == VX_EPI_SWIGLU) nt = std::max(nt, 2);
+        const int G = (int)(K / 64);
+        // prefer narrower column blocks when the grid would be too small
+        while (nt > (epi == VX_EPI_SWIGLU ? 2 : 1) &&
+               vx_cdiv(N, kWaves * nt * 16) * p.m_blocks * std::max(1, G / kChunkGroups) < target)
+            nt /= 2;
+        nt = env_int("VX_QMM_NT", nt);
+        p.NT = nt;
+        p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 16);
+        const int items = p.col_blocks * p.m_blocks;
+        int splits = std::max(1, target / std::max(1, items));
+        splits = std::min(splits, std::max(1, G / kChunkGroups));
+        splits = env_int("VX_QMM_SPLITS", splits);
+        splits = std::max(1, std::min(splits, G / kChunkGroups));
+        int gps = (int)vx_cdiv(G, splits);
+        gps = (int)vx_cdiv(gps, kChunkGroups) * kChunkGroups;
         splits = (int)vx_cdiv(G, gps);
+        // bound the partial-sum workspace
+        while (splits > 1 && (size_t)splits * M * N * 4 > kMaxPartialBytes) {
+            gps += kChunkGroups;
+            splits = (int)vx_cdiv(G, gps);
+        }
+        p.splits = splits;
+        p.gps = gps;
     }
-    p.splits = splits;
-    p.gps = gps;
-    p.total_items = p.col_blocks * splits;
+    p.total_items = p.col_blocks * p.splits;
     p.per_xcd = (int)vx_cdiv(p.total_items, 8);
-    p.partial_bytes = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+    p.partial_bytes = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
     return p;
+}
+
+void launch_reduce(const QmmArgs &a, const Plan &p, hipStream_t st) {
+    if (p.splits > 1) {
+        const int64_t outs = (int64_t)a.M * (a.epi == VX_EPI_SWIGLU ? a.N / 2 : a.N);
+        hipLaunchKernelGGL(qmm_reduce_kernel, dim3((unsigned)vx_cdiv(outs, 256)), dim3(256), 0, st, a);
+    }
+}
+
+template <int MT, int NT, bool PACKED>
+void launch_stream(const QmmArgs &a, const Plan &p, hipStream_t st) {
+    dim3 grid(p.per_xcd * 8, p.m_blocks);
+    hipLaunchKernelGGL((qmm_f16_stream_kernel<MT, NT, stream_depth(MT), PACKED>), grid, dim3(256), 0, st, a);
+    launch_reduce(a, p, st);
+}
+
+template <bool PACKED>
+int dispatch_stream(const QmmArgs &a, const Plan &p, hipStream_t st) {
+#define VX_CASE(mt, nt)                           \
+    if (p.MT == mt && p.NT == nt) {               \
+        launch_stream<mt, nt, PACKED>(a, p, st);  \
+        return 0;                                 \
+    }
+    VX_CASE(1, 1) VX_CASE(1, 2) VX_CASE(1, 4)
+    VX_CASE(2, 1) VX_CASE(2, 2) VX_CASE(2, 4)
+    VX_CASE(3, 1) VX_CASE(3, 2) VX_CASE(3, 4)
+    VX_CASE(4, 1) VX_CASE(4, 2) VX_CASE(4, 4)
+    VX_CASE(5, 1) VX_CASE(5, 2) VX_CASE(5, 4)
+#undef VX_CASE
+    return set_error("qmm: no streaming kernel for tile plan");
 }
 
 template <int MT, int NT, bool XBF>
 void launch_fast(const QmmArgs &a, const Plan &p, hipStream_t st) {
     dim3 grid(p.per_xcd * 8, p.m_blocks);
     hipLaunchKernelGGL((qmm_int4_kernel<MT, NT, XBF>), grid, dim3(256), 0, st, a);
-    if (p.splits > 1) {
-        const int64_t outs = (int64_t)a.M * (a.epi == VX_EPI_SWIGLU ? a.N / 2 : a.N);
-        hipLaunchKernelGGL(qmm_reduce_kernel, dim3((unsigned)vx_cdiv(outs, 256)), dim3(256), 0, st, a);
-    }
+    launch_reduce(a, p, st);
 }
 
 template <bool XBF>
@@ -449,24 +803,29 @@ int dispatch_fast(const QmmArgs &a, const Plan &p, hipStream_t st) {
     return set_error("qmm: no kernel for tile plan");
 }
 
-bool fast_ok(int64_t K, int64_t gs, const void *x, const void *w, const void *s, const void *b) {
-    return gs == 64 && K % 256 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 8) == 0 &&
-           ((uintptr_t)s % 8) == 0 && ((uintptr_t)b % 8) == 0;
+// Operand requirements of the tiled kernels: f16 activations take the
+// streaming kernel (K % 128, 16-byte weight rows), bf16 the LDS-chunked one.
+bool fast_ok(int dt, int64_t K, int64_t gs, const void *x, const void *w, const void *s, const void *b) {
+    if (gs != 64 || ((uintptr_t)x % 16) != 0) return false;
+    if (dt == VX_F16)
+        return K % 128 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)s % 4) == 0 && ((uintptr_t)b % 4) == 0;
+    return K % 256 == 0 && ((uintptr_t)w % 8) == 0 && ((uintptr_t)s % 8) == 0 && ((uintptr_t)b % 8) == 0;
 }
 
 }  // namespace
 
+// Workspace of the f16 (streaming) path.
 size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi) {
-    if (k % 256 != 0) return kCounterBytes;
-    Plan p = make_plan(m, n, k, epi);
+    if (k % 128 != 0) return kCounterBytes;
+    Plan p = make_plan(m, n, k, epi, true);
     return kCounterBytes + p.partial_bytes;
 }
 
 int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, void *y,
                const void *resid, int64_t M, int64_t N, int64_t K, int x_dt, int x_shift,
                int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
-               hipStream_t st) {
-    Plan p = make_plan(M, N, K, epi);
+               hipStream_t st, bool packed = false) {
+    Plan p = make_plan(M, N, K, epi, x_dt == VX_F16);
     if (epi == VX_EPI_SWIGLU && (N % 32 != 0 || p.NT % 2 != 0))
         return set_error("qmm swiglu: N must be a multiple of 32 with paired tiles");
     void *ws = workspace;
@@ -491,6 +850,8 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
     a.G = (int)(K / 64);
     a.splits = p.splits;
     a.gps = p.gps;
+    a.S = (int)(K / 128);
+    a.sps = p.sps;
     a.col_blocks = p.col_blocks;
     a.m_blocks = p.m_blocks;
     a.per_xcd = p.per_xcd;
@@ -500,7 +861,9 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
     a.y_dt = y_dt;
     a.acc_scale = ldexpf(1.0f, x_shift);
     a.store_scale = ldexpf(1.0f, -y_shift);
-    int rc = x_dt == VX_BF16 ? dispatch_fast<true>(a, p, st) : dispatch_fast<false>(a, p, st);
+    if (!p.stream && x_dt != VX_BF16) return set_error("qmm: the chunked kernel takes bf16 activations only");
+    int rc = p.stream ? (packed ? dispatch_stream<true>(a, p, st) : dispatch_stream<false>(a, p, st))
+                      : dispatch_fast<true>(a, p, st);
     if (rc) return rc;
     VX_HIP(hipGetLastError());
     return 0;
@@ -513,18 +876,51 @@ int qmm_fast(const void *x, const uint32_t *w, const void *s, const void *b, voi
                       ws_bytes, st);
 }
 
-// f16 activations (optionally stored as X * 2^-x_shift); the result is scaled
-// by 2^x_shift, rounded to round_dt, and stored as value * 2^-y_shift.
-int qmm_fast_scaled(const void *x, const uint32_t *w, const void *s, const void *b, void *y,
-                    const void *resid, int64_t M, int64_t N, int64_t K, int x_shift, int y_shift,
-                    int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes, hipStream_t st) {
-    return qmm_launch(x, w, s, b, y, resid, M, N, K, VX_F16, x_shift, y_shift, round_dt, y_dt, epi,
-                      workspace, ws_bytes, st);
+size_t qmm_packed_bytes(int64_t n, int64_t k) { return (size_t)(n / 16) * (size_t)(k / 128) * kPackBlock; }
+
+int qmm_pack(const uint32_t *w, const void *s, const void *b, void *out, int64_t N, int64_t K, hipStream_t st) {
+    if (N % 16 != 0 || K % 128 != 0) return set_error("qmm pack: N must be a multiple of 16 and K of 128");
+    if (((uintptr_t)w % 16) != 0 || ((uintptr_t)out % 16) != 0) return set_error("qmm pack: misaligned operand");
+    const int64_t blocks = (N / 16) * (K / 128);
+    if (blocks == 0) return 0;
+    hipLaunchKernelGGL(qmm_pack_kernel, dim3((unsigned)blocks), dim3(64), 0, st, w, (const uint16_t *)s,
+                       (const uint16_t *)b, (uint8_t *)out, (int)N, (int)K);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+// GEMM over packed weights (f16 activations, optionally X * 2^-x_shift; result
+// scaled by 2^x_shift, rounded to round_dt, stored as value * 2^-y_shift).
+int qmm_packed(const void *x, const void *packed, void *y, const void *resid, int64_t M, int64_t N, int64_t K,
+               int x_shift, int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
+               hipStream_t st) {
+    if (N % 16 != 0 || K % 128 != 0) return set_error("qmm packed: N must be a multiple of 16 and K of 128");
+    if (((uintptr_t)x % 16) != 0 || ((uintptr_t)packed % 16) != 0) return set_error("qmm packed: misaligned operand");
+    return qmm_launch(x, (const uint32_t *)packed, nullptr, nullptr, y, resid, M, N, K, VX_F16, x_shift, y_shift,
+                      round_dt, y_dt, epi, workspace, ws_bytes, st, true);
 }
 
 }  // namespace vx
 
 using namespace vx;
+
+extern "C" size_t vx_qmm_packed_size(int64_t n, int64_t k) { return qmm_packed_bytes(n, k); }
+
+extern "C" int vx_qmm_pack_4bit(const uint32_t *qweight, const void *scales, const void *biases, void *packed,
+                                int64_t n, int64_t k, void *stream) {
+    VX_REQUIRE(qweight && scales && biases && packed, "qmm_pack_4bit: null tensor");
+    return qmm_pack(qweight, scales, biases, packed, n, k, (hipStream_t)stream);
+}
+
+extern "C" int vx_qmm_4bit_packed(const void *x, const void *packed, void *y, const void *residual, int64_t m,
+                                  int64_t n, int64_t k, int x_shift, int round_dtype, int y_dtype, int epilogue,
+                                  void *workspace, size_t workspace_bytes, void *stream) {
+    VX_REQUIRE(x && packed && y, "qmm_4bit_packed: null tensor");
+    VX_REQUIRE(epilogue != VX_EPI_RESIDUAL || residual, "qmm_4bit_packed: residual epilogue needs R");
+    if (m == 0 || n == 0) return 0;
+    return qmm_packed(x, packed, y, residual, m, n, k, x_shift, 0, round_dtype, y_dtype, epilogue, workspace,
+                      workspace_bytes, (hipStream_t)stream);
+}
 
 extern "C" int vx_qmm_4bit(const void *x, const uint32_t *qweight, const void *scales,
                            const void *biases, const void *bias, void *y, int64_t m, int64_t n,
@@ -538,7 +934,7 @@ extern "C" int vx_qmm_4bit(const void *x, const uint32_t *qweight, const void *s
     VX_REQUIRE(x && qweight && scales && biases && y, "qmm_4bit: null tensor");
     if (m == 0 || n == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype != VX_F32 && fast_ok(k, group_size, x, qweight, scales, biases) && m * n < ((int64_t)1 << 31)) {
+    if (dtype != VX_F32 && fast_ok(dtype, k, group_size, x, qweight, scales, biases) && m * n < ((int64_t)1 << 31)) {
         VX_TRY(qmm_fast(x, qweight, scales, biases, y, nullptr, m, n, k, dtype, 0, dtype, dtype,
                         VX_EPI_STORE, nullptr, 0, st));
         if (bias) {
@@ -569,10 +965,10 @@ extern "C" int vx_qmm_4bit_ex(const void *x, const uint32_t *qweight, const void
                               int round_dtype, int y_dtype, int epilogue, void *workspace,
                               size_t workspace_bytes, void *stream) {
     VX_REQUIRE(group_size == 64, "qmm_4bit_ex: group_size must be 64");
-    VX_REQUIRE(k % 256 == 0, "qmm_4bit_ex: K must be a multiple of 256");
+    VX_REQUIRE(k % 128 == 0, "qmm_4bit_ex: K must be a multiple of 128");
     VX_REQUIRE(x && qweight && scales && biases && y, "qmm_4bit_ex: null tensor");
     VX_REQUIRE(epilogue != VX_EPI_RESIDUAL || residual, "qmm_4bit_ex: residual epilogue needs R");
-    VX_REQUIRE(fast_ok(k, group_size, x, qweight, scales, biases), "qmm_4bit_ex: misaligned operand");
+    VX_REQUIRE(fast_ok(VX_F16, k, group_size, x, qweight, scales, biases), "qmm_4bit_ex: misaligned operand");
     if (m == 0 || n == 0) return 0;
     return qmm_fast(x, qweight, scales, biases, y, residual, m, n, k, VX_F16, x_shift, round_dtype,
                     y_dtype, epilogue, workspace, workspace_bytes, (hipStream_t)stream);

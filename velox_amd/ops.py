@@ -78,6 +78,31 @@ def qmm_4bit_ex(x, qweight, scales, biases, out, residual=None, x_shift=0, round
     return out
 
 
+def qmm_pack_4bit(qweight, scales, biases):
+    """Packed copy of MLX int4 g64 weights (f16 scales/biases) for qmm_4bit_packed."""
+    n, kp = qweight.shape
+    k = kp * 8
+    _need(n % 16 == 0 and k % 128 == 0, f"qmm_pack_4bit: N={n} must be a multiple of 16 and K={k} of 128")
+    _need(tuple(scales.shape) == (n, k // 64) and tuple(biases.shape) == (n, k // 64),
+          "qmm_pack_4bit: scales/biases must be [N, K/64]")
+    _contig("qmm_pack_4bit", qweight=qweight, scales=scales, biases=biases)
+    out = torch.empty(int(lib.vx_qmm_packed_size(n, k)), dtype=torch.uint8, device=qweight.device)
+    check(lib.vx_qmm_pack_4bit(qweight.data_ptr(), scales.data_ptr(), biases.data_ptr(), out.data_ptr(), n, k,
+                               _stream()))
+    return out
+
+
+def qmm_4bit_packed(x, packed, n, out, residual=None, x_shift=0, round_dtype=BF16, epilogue=EPI_STORE,
+                    workspace=None):
+    """qmm_4bit_ex over packed weights (see qmm_pack_4bit)."""
+    m, k = x.shape
+    ws = _p(workspace)
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(lib.vx_qmm_4bit_packed(x.data_ptr(), packed.data_ptr(), out.data_ptr(), _p(residual), m, n, k, x_shift,
+                                 round_dtype, _DT[out.dtype], epilogue, ws, wsb, _stream()))
+    return out
+
+
 def paged_prefill_attention(q, k_pool, v_pool, block_table, cu_seqlens, seq_id_per_q, kv_offsets, scale,
                             sliding_window=0, tree_mask=None):
     """paged_prefill_attention (metal_kernels.rs:1680-1690), plus an optional per-row
