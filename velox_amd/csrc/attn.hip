@@ -29,6 +29,7 @@ namespace vx {
 namespace {
 
 constexpr int kKeyBlock = 64;
+constexpr int kAttnWaves = 4;  // waves per workgroup, splitting an item's key blocks
 constexpr size_t kAttnCounterBytes = 65536;
 
 struct AttnArgs {
@@ -82,15 +83,30 @@ __device__ __forceinline__ void row_info(const AttnArgs &a, int seq, int &r_seq,
 }
 
 // D: head dim (multiple of 32, <= 256); QT: query tiles of 16 per wave.
+// Four waves per workgroup share one item; wave w takes the 64-key blocks
+// w, w+4, ... of the item's key range, and the four partial (m, l, O) merge
+// through LDS in wave order (deterministic) before the output / split
+// partial is written.
 template <int KT, int D, int QT>
-__global__ __launch_bounds__(64) void paged_attn_kernel(AttnArgs a) {
+constexpr size_t attn_lds_bytes() {
+    constexpr size_t vt = (size_t)kAttnWaves * D * (kKeyBlock + 4) * 2;
+    constexpr size_t comb = (size_t)(kAttnWaves - 1) * ((D / 16) * QT * 4 + 2 * QT) * 64 * 4;
+    return vt > comb ? vt : comb;
+}
+
+template <int KT, int D, int QT>
+__global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     typedef typename MfmaT<KT>::frag frag;
     constexpr int DK = D / 32;  // MFMA k-steps over head_dim
     constexpr int DT = D / 16;  // output row tiles of O^T
     constexpr int VT_STRIDE = kKeyBlock + 4;  // halves per transposed V row (bank spread)
-    __shared__ uint16_t vt[D * VT_STRIDE];
+    constexpr int CSLOTS = DT * QT * 4 + 2 * QT;  // floats per lane in the wave merge
+    // per-wave V^T tiles during the key loop; the merge buffers afterwards
+    __shared__ __attribute__((aligned(16))) unsigned char smem[attn_lds_bytes<KT, D, QT>()];
 
-    const int lane = threadIdx.x;
+    const int wave = threadIdx.x >> 6;
+    uint16_t *vt = (uint16_t *)smem + wave * D * VT_STRIDE;
+    const int lane = threadIdx.x & 63;
     const int lq = lane & 15;
     const int lg = lane >> 4;
     int item = blockIdx.x;
@@ -154,7 +170,7 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(AttnArgs a) {
     const uint32_t *btr = a.bt + (int64_t)seq * a.max_blocks;
     const int win = (int)a.window;
 
-    for (int kb = k_lo; kb < k_hi; kb += kKeyBlock) {
+    for (int kb = k_lo + wave * kKeyBlock; kb < k_hi; kb += kAttnWaves * kKeyBlock) {
         // ---- S^T for 64 keys: 4 tiles of 16 keys
         floatx4 s[4][QT];
 #pragma unroll
@@ -180,7 +196,8 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(AttnArgs a) {
             const int blk = min(key / a.ps, a.max_blocks - 1);
             const int page = min((int)btr[blk], a.num_pages - 1);
             const uint16_t *vr = (const uint16_t *)a.v + page * page_stride + hk * head_stride + (int64_t)(key % a.ps) * D;
-            __syncthreads();
+            // the wave's own V^T tile: LDS operations of one wave complete in order
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int c = 0; c < D / 8; c++) {
                 uint4 raw = *(const uint4 *)(vr + c * 8);
@@ -252,7 +269,7 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(AttnArgs a) {
                 pf[qt][st] = *(frag *)tmp;
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
         // ---- O^T += V^T . P^T ; A element e <-> key 32*st + 4*lg + (e < 4 ? e : 12 + e)
 #pragma unroll
         for (int i = 0; i < DT; i++) {
@@ -265,6 +282,45 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
                 for (int qt = 0; qt < QT; qt++) o[i][qt] = MfmaT<KT>::mma(vf, pf[qt][st], o[i][qt]);
             }
+        }
+    }
+
+    // ---- merge the four waves' partials (key order = wave order) into wave 0
+    __syncthreads();  // every wave is done with its V^T tile
+    float *comb = (float *)smem;
+    if (wave > 0) {
+        float *dst = comb + (size_t)(wave - 1) * CSLOTS * 64 + lane;
+        int slot = 0;
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+            dst[(slot++) * 64] = m_run[qt];
+            dst[(slot++) * 64] = l_run[qt];
+#pragma unroll
+            for (int i = 0; i < DT; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) dst[(slot++) * 64] = o[i][qt][r];
+        }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; w++) {
+        const float *src = comb + (size_t)(w - 1) * CSLOTS * 64 + lane;
+        int slot = 0;
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+            const float mw = src[(slot++) * 64];
+            const float lw = src[(slot++) * 64];
+            const float m_new = fmaxf(m_run[qt], mw);
+            const bool dead = m_new == -__builtin_inff();
+            const float fa = dead ? 1.f : exp2f(m_run[qt] - m_new);
+            const float fb = dead ? 0.f : exp2f(mw - m_new);
+            l_run[qt] = l_run[qt] * fa + lw * fb;
+            m_run[qt] = m_new;
+#pragma unroll
+            for (int i = 0; i < DT; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) o[i][qt][r] = o[i][qt][r] * fa + src[(slot++) * 64] * fb;
         }
     }
 
@@ -409,7 +465,7 @@ __global__ void zero_u16_kernel(uint16_t *p, int64_t n) {
 
 template <int KT, int D, int QT>
 void launch_attn(const AttnArgs &a, int64_t n_items, hipStream_t st) {
-    hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT>), dim3((unsigned)n_items), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT>), dim3((unsigned)n_items), dim3(64 * kAttnWaves), 0, st, a);
 }
 
 template <int KT>
@@ -477,13 +533,14 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
     if (QT == 3) QT = 4;
     a.qr = std::max(1, (QT * 16) / a.G);
     a.n_qtiles = (int)vx_cdiv(max_rows, a.qr);
-    // KV split: aim for ~2 waves per SIMD across the chip
+    // KV split across workgroups (each workgroup's four waves already split
+    // its range): aim for ~2 workgroups per CU, at least one key block per wave
     const int64_t base_items = n_seqs * h_kv * a.n_qtiles;
     const int64_t max_keys = std::max<int64_t>(1, max_kv);
-    const int64_t target = 4LL * device_cu_count() * 2;
+    const int64_t target = 2LL * device_cu_count();
     int64_t splits = std::max<int64_t>(1, target / std::max<int64_t>(1, base_items));
     int64_t chunk = vx_cdiv(vx_cdiv(max_keys, splits), kKeyBlock) * kKeyBlock;
-    chunk = std::max<int64_t>(chunk, 4 * kKeyBlock);
+    chunk = std::max<int64_t>(chunk, kAttnWaves * kKeyBlock);
     splits = vx_cdiv(max_keys, chunk);
     a.chunk = (int)chunk;
     a.n_splits = (int)splits;

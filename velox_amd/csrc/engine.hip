@@ -120,11 +120,16 @@ int embed_launch(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_
                  int64_t vocab, hipStream_t st);
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
                    int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
-int qk_rope_scatter_launch(const uint16_t *qkv, const uint16_t *qn, const uint16_t *kn,
-                           const uint16_t *cos_t, const uint16_t *sin_t, const uint32_t *pos,
-                           const uint32_t *pages, const uint32_t *slots, uint16_t *qout,
-                           uint16_t *kp, uint16_t *vp, int64_t rows, int HQ, int HK, int D, int ps,
-                           float eps, int kv_dt, hipStream_t st);
+int qkv_partial_rope_scatter_launch(const float *partial, int splits, const uint16_t *qn, const uint16_t *kn,
+                                    const uint16_t *cos_t, const uint16_t *sin_t, const uint32_t *pos,
+                                    const uint32_t *pages, const uint32_t *slots, uint16_t *qout, uint16_t *kp,
+                                    uint16_t *vp, int64_t rows, int HQ, int HK, int D, int ps, float eps, int kv_dt,
+                                    hipStream_t st);
+int residual_rmsnorm_launch(const float *partial, int splits, float acc_scale, uint16_t *h, const uint16_t *ln,
+                            uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
+size_t qmm_partial_ws_bytes(int64_t M, int64_t N, int64_t K);
+int qmm_packed_partial(const void *x, const void *packed, int64_t M, int64_t N, int64_t K, void *workspace,
+                       size_t ws_bytes, int *splits, const float **partial, hipStream_t st);
 
 // ---------------------------------------------------------------------------
 // host-side 16-bit conversions (RNE), identical to the device converts
@@ -392,7 +397,7 @@ struct vx_model {
     uint16_t *cos_t = nullptr, *sin_t = nullptr;  // bf16 [max_pos, D/2]
     std::vector<void *> allocs;
     // activations
-    DevBuf h, xn, qkv, q, attn, act, ids, meta, ws;
+    DevBuf h, xn, q, attn, act, ids, meta, ws;
     int64_t cap_rows = 0;
     ~vx_model() {
         for (void *p : allocs) (void)hipFree(p);
@@ -483,6 +488,7 @@ extern "C" int vx_model_create(const vx_qwen3_config *cfg, const vx_weights_host
     VX_REQUIRE(cfg->group_size == 64, "model: only MLX int4 group_size 64 is supported");
     VX_REQUIRE(H % 256 == 0 && F % 256 == 0 && (HQ * D) % 256 == 0, "model: hidden/inter/heads*head_dim must be multiples of 256");
     VX_REQUIRE(HK > 0 && HQ % HK == 0, "model: n_heads must be divisible by n_kv_heads");
+    VX_REQUIRE(H <= 8192, "model: hidden size above 8192 is not supported");
     VX_REQUIRE(D % 32 == 0 && D <= 256, "model: head_dim must be a multiple of 32 and <= 256");
     VX_REQUIRE(F % 16 == 0, "model: intermediate size must be a multiple of 16");
     VX_REQUIRE(cfg->vocab % 16 == 0, "model: vocab must be a multiple of 16");
@@ -631,7 +637,6 @@ int ensure_buffers(vx_model *m, int64_t rows) {
     const int64_t R = std::max<int64_t>(rows, 16);
     VX_TRY(m->h.ensure(R * H * 2));
     VX_TRY(m->xn.ensure(R * std::max({H, QW, F}) * 2));
-    VX_TRY(m->qkv.ensure(R * (QW + 2 * KW) * 2));
     VX_TRY(m->q.ensure(R * QW * 2));
     VX_TRY(m->attn.ensure(R * QW * 2));
     VX_TRY(m->act.ensure(R * F * 2));
@@ -645,10 +650,10 @@ size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int
     const vx_qwen3_config &c = m->cfg;
     const int64_t H = c.hidden, F = c.inter, QW = c.n_heads * c.head_dim, KW = c.n_kv_heads * c.head_dim;
     size_t need = 0;
-    need = std::max(need, qmm_workspace_bytes(rows, QW + 2 * KW, H, VX_EPI_STORE));
-    need = std::max(need, qmm_workspace_bytes(rows, H, QW, VX_EPI_RESIDUAL));
+    need = std::max(need, qmm_partial_ws_bytes(rows, QW + 2 * KW, H));
+    need = std::max(need, qmm_partial_ws_bytes(rows, H, QW));
     need = std::max(need, qmm_workspace_bytes(rows, 2 * F, H, VX_EPI_SWIGLU));
-    need = std::max(need, qmm_workspace_bytes(rows, H, F, VX_EPI_RESIDUAL));
+    need = std::max(need, qmm_partial_ws_bytes(rows, H, F));
     need = std::max(need, qmm_workspace_bytes(logit_rows, c.vocab, H, VX_EPI_STORE));
     // attention: upper bound on its split plan (see paged_attention_launch)
     const int64_t G = c.n_heads / c.n_kv_heads;
@@ -681,7 +686,7 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     const uint32_t *bt = (const uint32_t *)(meta_dev + meta.o_bt);
     const uint64_t *mask = meta.tree ? (const uint64_t *)(meta_dev + meta.o_mask) : nullptr;
     const uint32_t *last = (const uint32_t *)(meta_dev + meta.o_last);
-    uint16_t *h = (uint16_t *)m->h.p, *xn = (uint16_t *)m->xn.p, *qkv = (uint16_t *)m->qkv.p;
+    uint16_t *h = (uint16_t *)m->h.p, *xn = (uint16_t *)m->xn.p;
     uint16_t *q = (uint16_t *)m->q.p, *attn = (uint16_t *)m->attn.p, *act = (uint16_t *)m->act.p;
     const float scale = 1.0f / sqrtf((float)D);
 
@@ -689,23 +694,30 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
         ProfScope ps_(prof, st, PC_OTHER, 0.0);
         VX_TRY(embed_launch(ids_dev, m->embed, h, R, H, c.vocab, st));
     }
+    // Per layer: qkv projection (split partials) -> q/k norm + RoPE + KV write
+    // (finishing the projection) -> attention -> o projection (partials) ->
+    // residual + ln2 norm -> gate|up with the SwiGLU finish -> down
+    // projection (partials) -> residual + the next norm (next layer's ln1,
+    // or the final norm when every row goes to the LM head).
+    {
+        ProfScope ps_(prof, st, PC_OTHER, 0.0);
+        VX_TRY(rmsnorm_launch(h, m->layers[0].ln1, xn, nullptr, R, H, eps, VX_F16, st));
+    }
+    int splits = 0;
+    const float *part = nullptr;
     for (int64_t l = 0; l < m->L; l++) {
         const LayerDev &ly = m->layers[l];
         uint16_t *kp = (uint16_t *)vx_pages_pool(pg, l, 0);
         uint16_t *vp = (uint16_t *)vx_pages_pool(pg, l, 1);
         {
-            ProfScope ps_(prof, st, PC_OTHER, 0.0);
-            VX_TRY(rmsnorm_launch(h, ly.ln1, xn, nullptr, R, H, eps, VX_F16, st));
-        }
-        {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, QW + 2 * KW, H, false));
-            VX_TRY(qmm_packed(xn, ly.qkv.packed, qkv, nullptr, R, QW + 2 * KW, H, 0, 0, VX_BF16,
-                                   VX_BF16, VX_EPI_STORE, ws, ws_bytes, st));
+            VX_TRY(qmm_packed_partial(xn, ly.qkv.packed, R, QW + 2 * KW, H, ws, ws_bytes, &splits, &part, st));
         }
         {
             ProfScope ps_(prof, st, PC_OTHER, 0.0);
-            VX_TRY(qk_rope_scatter_launch(qkv, ly.qn, ly.kn, m->cos_t, m->sin_t, pos, pages, slots, q, kp, vp, R,
-                                          (int)HQ, (int)HK, (int)D, (int)pg->page_size, eps, VX_F16, st));
+            VX_TRY(qkv_partial_rope_scatter_launch(part, splits, ly.qn, ly.kn, m->cos_t, m->sin_t, pos, pages, slots,
+                                                   q, kp, vp, R, (int)HQ, (int)HK, (int)D, (int)pg->page_size, eps,
+                                                   VX_F16, st));
         }
         {
             ProfScope ps_(prof, st, PC_ATTN, kv_bytes_per_layer + 4.0 * R * QW);
@@ -715,28 +727,33 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, H, QW, true));
-            VX_TRY(qmm_packed(attn, ly.o.packed, h, h, R, H, QW, 0, 0, VX_BF16, VX_BF16,
-                                   VX_EPI_RESIDUAL, ws, ws_bytes, st));
+            VX_TRY(qmm_packed_partial(attn, ly.o.packed, R, H, QW, ws, ws_bytes, &splits, &part, st));
         }
         {
             ProfScope ps_(prof, st, PC_OTHER, 0.0);
-            VX_TRY(rmsnorm_launch(h, ly.ln2, xn, nullptr, R, H, eps, VX_F16, st));
+            VX_TRY(residual_rmsnorm_launch(part, splits, 1.0f, h, ly.ln2, xn, R, H, eps, VX_F16, st));
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, 2 * F, H, false) - 2.0 * R * F);
             VX_TRY(qmm_packed(xn, ly.gu.packed, act, nullptr, R, 2 * F, H, 0, kMlpShift, VX_BF16,
-                                   VX_F16, VX_EPI_SWIGLU, ws, ws_bytes, st));
+                              VX_F16, VX_EPI_SWIGLU, ws, ws_bytes, st));
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, H, F, true));
-            VX_TRY(qmm_packed(act, ly.down.packed, h, h, R, H, F, kMlpShift, 0, VX_BF16,
-                                   VX_BF16, VX_EPI_RESIDUAL, ws, ws_bytes, st));
+            VX_TRY(qmm_packed_partial(act, ly.down.packed, R, H, F, ws, ws_bytes, &splits, &part, st));
+        }
+        {
+            ProfScope ps_(prof, st, PC_OTHER, 0.0);
+            const bool last_layer = l + 1 == m->L;
+            const uint16_t *next_ln = !last_layer ? m->layers[l + 1].ln1 : (all_rows ? m->norm : nullptr);
+            VX_TRY(residual_rmsnorm_launch(part, splits, ldexpf(1.0f, kMlpShift), h, next_ln, xn, R, H, eps,
+                                           VX_F16, st));
         }
     }
     const int64_t lrows = all_rows ? R : meta.n_seqs;
-    {
+    if (!all_rows) {
         ProfScope ps_(prof, st, PC_OTHER, 0.0);
-        VX_TRY(rmsnorm_launch(h, m->norm, xn, all_rows ? nullptr : last, lrows, H, eps, VX_F16, st));
+        VX_TRY(rmsnorm_launch(h, m->norm, xn, last, lrows, H, eps, VX_F16, st));
     }
     {
         ProfScope ps_(prof, st, PC_QMM, qmm_bytes(lrows, c.vocab, H, false));

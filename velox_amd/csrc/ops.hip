@@ -24,94 +24,204 @@ __global__ void embed_kernel(const uint32_t *ids, const uint16_t *embed, uint16_
     for (int64_t i = threadIdx.x; i < H / 8; i += blockDim.x) dst[i] = src[i];
 }
 
-// y = round_bf16(x / sqrt(mean(x^2) + eps) * w), stored as f16 (exact carrier
-// of the bf16 value) for the next GEMM.  x, w in bf16.  rows optionally
-// gathered through row_idx (last row per sequence).
-__global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const uint16_t *x, const uint16_t *w,
-                                                          uint16_t *y, const uint32_t *row_idx,
-                                                          int64_t H, float eps, int out_dt) {
-    __shared__ float red[256];
-    const int64_t r = blockIdx.x;
-    const int64_t src_r = row_idx ? row_idx[r] : r;
-    const uint16_t *xr = x + src_r * H;
-    float s = 0.f;
-    for (int64_t i = threadIdx.x; i < H; i += 256) {
-        const float v = bf16_bits_to_f32(xr[i]);
-        s += v * v;
-    }
-    red[threadIdx.x] = s;
+constexpr int kMaxFusedSplits = 8;  // split partials a fused finish reads
+
+// Sum over the workgroup (threads = 64 * waves <= 1024), same value in every thread.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
-    for (int st = 128; st > 0; st >>= 1) {
-        if ((int)threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
-        __syncthreads();
-    }
-    const float m = sqrtf(red[0] / (float)H + eps);
-    for (int64_t i = threadIdx.x; i < H; i += 256) {
-        const float v = round_to<VX_BF16>(bf16_bits_to_f32(xr[i]) / m * bf16_bits_to_f32(w[i]));
-        if (out_dt == VX_F16)
-            y[r * H + i] = f32_to_f16_bits(v);
-        else
-            y[r * H + i] = f32_to_bf16_bits(v);
+    float t = 0.f;
+    for (int w = 0; w < nw; w++) t += red[w];
+    return t;
+}
+
+// Eight bf16 values (one 16-byte piece of a row) -> floats.
+__device__ __forceinline__ void bf16x8_unpack(uint4 v, float (&f)[8]) {
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[2 * e] = __uint_as_float(u[e] << 16);
+        f[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
     }
 }
 
-// Per row: q/k heads get the per-head RMSNorm (qwen3.rs:435-454) and RoPE at
-// rope_pos[row] (MSL :209-241, tables in bf16); q goes to qout and k, v are
-// written into the pools at (page_ids[row], slots[row]) (MSL :251-279), all in
-// the pool dtype (f16 pools carry the bf16-rounded values exactly).  One wave
-// per head.
+// y = round_bf16(x / m * w) for the thread's eight columns, m = sqrt(mean(x^2) + eps),
+// stored as f16 (exact carrier of the bf16 value) or bf16.
+__device__ __forceinline__ uint4 rms_apply8(const float (&x)[8], uint4 wv, float m, int out_dt) {
+    float w[8];
+    bf16x8_unpack(wv, w);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float a = round_to<VX_BF16>(x[2 * e] / m * w[2 * e]);
+        const float b = round_to<VX_BF16>(x[2 * e + 1] / m * w[2 * e + 1]);
+        o[e] = out_dt == VX_F16 ? ((uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16))
+                                : ((uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16));
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// y = round_bf16(x / sqrt(mean(x^2) + eps) * w) (candle RmsNorm in bf16), x, w
+// bf16, y as f16 carrier or bf16.  Rows optionally gathered through row_idx
+// (last row per sequence).  One workgroup per row, one thread per 8 columns;
+// the row and the weights are requested together up front.
+__global__ __launch_bounds__(1024) void rmsnorm_bf16_kernel(const uint16_t *x, const uint16_t *w, uint16_t *y,
+                                                           const uint32_t *row_idx, int H, float eps, int out_dt) {
+    __shared__ float red[16];
+    const int r = blockIdx.x;
+    const int i = threadIdx.x;
+    const bool live = i < H / 8;
+    const int64_t src_r = row_idx ? row_idx[r] : r;
+    const uint4 xv = live ? ((const uint4 *)(x + src_r * H))[i] : make_uint4(0u, 0u, 0u, 0u);
+    const uint4 wv = live ? ((const uint4 *)w)[i] : make_uint4(0u, 0u, 0u, 0u);
+    float f[8];
+    bf16x8_unpack(xv, f);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) s += f[e] * f[e];
+    const float m = sqrtf(block_sum(s, red) / (float)H + eps);
+    if (live) ((uint4 *)(y + (int64_t)r * H))[i] = rms_apply8(f, wv, m, out_dt);
+}
+
+// A projection's finish fused with the next RMSNorm, one workgroup per row:
+//   h[r, :] = round_bf16(h[r, :] + round_bf16(acc_scale * sum_sp partial[sp][r][:]))
+// (the RESIDUAL epilogue, partials summed in split order), written back as
+// bf16; then, when ln is given, y = RMSNorm(h) * ln as rmsnorm_bf16_kernel.
+__global__ __launch_bounds__(1024) void residual_rmsnorm_kernel(const float *partial, int splits, float acc_scale,
+                                                               uint16_t *hrow, const uint16_t *ln, uint16_t *y,
+                                                               int rows, int H, float eps, int out_dt) {
+    __shared__ float red[16];
+    const int r = blockIdx.x;
+    const int i = threadIdx.x;
+    const bool live = i < H / 8;
+    uint4 *hr = (uint4 *)(hrow + (int64_t)r * H);
+    const uint4 old = live ? hr[i] : make_uint4(0u, 0u, 0u, 0u);
+    const uint4 wv = (live && ln) ? ((const uint4 *)ln)[i] : make_uint4(0u, 0u, 0u, 0u);
+    float4 p[kMaxFusedSplits][2];
+#pragma unroll
+    for (int sp = 0; sp < kMaxFusedSplits; sp++) {
+        if (live && sp < splits) {
+            const float4 *pp = (const float4 *)(partial + ((int64_t)sp * rows + r) * H + 8 * i);
+            p[sp][0] = pp[0];
+            p[sp][1] = pp[1];
+        } else {
+            p[sp][0] = p[sp][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < kMaxFusedSplits; sp++) {
+        if (sp < splits) {
+            acc[0] += p[sp][0].x; acc[1] += p[sp][0].y; acc[2] += p[sp][0].z; acc[3] += p[sp][0].w;
+            acc[4] += p[sp][1].x; acc[5] += p[sp][1].y; acc[6] += p[sp][1].z; acc[7] += p[sp][1].w;
+        }
+    }
+    float hv[8];
+    bf16x8_unpack(old, hv);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e++) hv[e] = round_to<VX_BF16>(hv[e] + round_to<VX_BF16>(acc[e] * acc_scale));
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = (uint32_t)f32_to_bf16_bits(hv[2 * e]) | ((uint32_t)f32_to_bf16_bits(hv[2 * e + 1]) << 16);
+    if (live) hr[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    if (!ln) return;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) s += hv[e] * hv[e];
+    const float m = sqrtf(block_sum(s, red) / (float)H + eps);
+    if (live) ((uint4 *)(y + (int64_t)r * H))[i] = rms_apply8(hv, wv, m, out_dt);
+}
+
+// Per (row, head), one wave: q/k heads get the per-head RMSNorm
+// (qwen3.rs:435-454) and RoPE at rope_pos[row] (MSL :209-241, tables in
+// bf16); q goes to qout and k, v are written into the pools at
+// (page_ids[row], slots[row]) (MSL :251-279), all in the pool dtype (f16
+// pools carry the bf16-rounded values exactly).  Lane j holds the RoPE pair
+// (j, j + D/2).  With PARTIAL the qkv row is the sum of the projection's f32
+// split partials [splits][rows][N] in split order, rounded to bf16 as the
+// projection's store would (the projection's finish fused here).
+template <bool PARTIAL>
 __global__ __launch_bounds__(256) void qk_rope_scatter_kernel(
-    const uint16_t *qkv, const uint16_t *qn_w, const uint16_t *kn_w, const uint16_t *cos_t,
-    const uint16_t *sin_t, const uint32_t *rope_pos, const uint32_t *page_ids,
-    const uint32_t *slots, uint16_t *qout, uint16_t *k_pool, uint16_t *v_pool, int HQ, int HK,
+    const uint16_t *qkv, const float *partial, int splits, const uint16_t *qn_w, const uint16_t *kn_w,
+    const uint16_t *cos_t, const uint16_t *sin_t, const uint32_t *rope_pos, const uint32_t *page_ids,
+    const uint32_t *slots, uint16_t *qout, uint16_t *k_pool, uint16_t *v_pool, int rows, int HQ, int HK,
     int D, int ps, float eps, int kv_dt) {
-    const int64_t r = blockIdx.x;
-    const int wave = threadIdx.x >> 6;
+    const int NH = HQ + 2 * HK;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int QW = HQ * D, KW = HK * D;
-    const uint16_t *row = qkv + r * (int64_t)(QW + 2 * KW);
+    if (gw >= rows * NH) return;
+    const int r = gw / NH;
+    const int h = gw - r * NH;
+    const int QW = HQ * D, KW = HK * D, N = QW + 2 * KW;
+    const uint16_t *row = qkv + (int64_t)r * N;
+    auto val = [&](int c) -> float {
+        if constexpr (PARTIAL) {
+            float pv[kMaxFusedSplits];
+#pragma unroll
+            for (int sp = 0; sp < kMaxFusedSplits; sp++)
+                pv[sp] = sp < splits ? partial[((int64_t)sp * rows + r) * N + c] : 0.f;
+            float acc = 0.f;
+#pragma unroll
+            for (int sp = 0; sp < kMaxFusedSplits; sp++)
+                if (sp < splits) acc += pv[sp];
+            return round_to<VX_BF16>(acc);
+        } else {
+            return bf16_bits_to_f32(row[c]);
+        }
+    };
     const int half = D / 2;
-    const uint32_t pos = rope_pos[r];
     const int64_t page = page_ids[r];
     const int slot = (int)slots[r];
-    for (int h = wave; h < HQ + 2 * HK; h += 4) {
-        if (h >= HQ + HK) {  // v head: plain copy
-            const int hv = h - HQ - HK;
-            const uint16_t *src = row + QW + KW + hv * D;
-            uint16_t *dst = v_pool + ((page * HK + hv) * ps + slot) * (int64_t)D;
-            for (int i = lane; i < D; i += 64) {
-                const float v = bf16_bits_to_f32(src[i]);
-                dst[i] = kv_dt == VX_F16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
-            }
-            continue;
-        }
-        const bool is_q = h < HQ;
-        const uint16_t *src = is_q ? row + h * D : row + QW + (h - HQ) * D;
-        const uint16_t *nw = is_q ? qn_w : kn_w;
-        // per-head RMSNorm over D
-        float ss = 0.f;
+    if (h >= HQ + HK) {  // v head: plain copy
+        const int hv = h - HQ - HK;
+        const int c0 = QW + KW + hv * D;
+        uint16_t *dst = v_pool + ((page * HK + hv) * ps + slot) * (int64_t)D;
         for (int i = lane; i < D; i += 64) {
-            const float v = bf16_bits_to_f32(src[i]);
-            ss += v * v;
+            const float v = val(c0 + i);
+            dst[i] = kv_dt == VX_F16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
         }
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-        const float m = sqrtf(ss / (float)D + eps);
-        uint16_t *dst = is_q ? qout + (r * HQ + h) * (int64_t)D
-                             : k_pool + ((page * HK + (h - HQ)) * ps + slot) * (int64_t)D;
-        for (int j = lane; j < half; j += 64) {
-            const float x1 = round_to<VX_BF16>(bf16_bits_to_f32(src[j]) / m * bf16_bits_to_f32(nw[j]));
-            const float x2 = round_to<VX_BF16>(bf16_bits_to_f32(src[j + half]) / m * bf16_bits_to_f32(nw[j + half]));
-            const float c = bf16_bits_to_f32(cos_t[(int64_t)pos * half + j]);
-            const float s = bf16_bits_to_f32(sin_t[(int64_t)pos * half + j]);
-            const float y1 = round_to<VX_BF16>(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
-            const float y2 = round_to<VX_BF16>(__fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c)));
-            if (kv_dt == VX_F16) {
-                dst[j] = f32_to_f16_bits(y1);
-                dst[j + half] = f32_to_f16_bits(y2);
-            } else {
-                dst[j] = f32_to_bf16_bits(y1);
-                dst[j + half] = f32_to_bf16_bits(y2);
-            }
+        return;
+    }
+    const uint32_t pos = rope_pos[r];
+    const bool is_q = h < HQ;
+    const int c0 = is_q ? h * D : QW + (h - HQ) * D;
+    const uint16_t *nw = is_q ? qn_w : kn_w;
+    // per-head RMSNorm over D: lane holds pairs (j, j + half) for j = lane, lane + 64, ...
+    constexpr int kMaxPairs = 2;  // D <= 256
+    float x1[kMaxPairs], x2[kMaxPairs];
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < kMaxPairs; p++) {
+        const int j = lane + 64 * p;
+        x1[p] = j < half ? val(c0 + j) : 0.f;
+        x2[p] = j < half ? val(c0 + j + half) : 0.f;
+        ss += x1[p] * x1[p];
+        ss += x2[p] * x2[p];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float m = sqrtf(ss / (float)D + eps);
+    uint16_t *dst = is_q ? qout + ((int64_t)r * HQ + h) * D
+                         : k_pool + ((page * HK + (h - HQ)) * ps + slot) * (int64_t)D;
+#pragma unroll
+    for (int p = 0; p < kMaxPairs; p++) {
+        const int j = lane + 64 * p;
+        if (j >= half) break;
+        const float a = round_to<VX_BF16>(x1[p] / m * bf16_bits_to_f32(nw[j]));
+        const float b = round_to<VX_BF16>(x2[p] / m * bf16_bits_to_f32(nw[j + half]));
+        const float c = bf16_bits_to_f32(cos_t[(int64_t)pos * half + j]);
+        const float s = bf16_bits_to_f32(sin_t[(int64_t)pos * half + j]);
+        const float y1 = round_to<VX_BF16>(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)));
+        const float y2 = round_to<VX_BF16>(__fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c)));
+        if (kv_dt == VX_F16) {
+            dst[j] = f32_to_f16_bits(y1);
+            dst[j + half] = f32_to_f16_bits(y2);
+        } else {
+            dst[j] = f32_to_bf16_bits(y1);
+            dst[j + half] = f32_to_bf16_bits(y2);
         }
     }
 }
@@ -668,7 +778,11 @@ int embed_launch(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_
 
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
                    int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st) {
-    hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, w, y, row_idx, H, eps, out_dt);
+    if (H % 8 != 0 || H > 8 * 1024) return set_error("rmsnorm: hidden size must be a multiple of 8 and <= 8192");
+    if (rows == 0) return 0;
+    const unsigned threads = (unsigned)vx_cdiv(H / 8, 64) * 64;
+    hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(threads), 0, st, x, w, y, row_idx, (int)H,
+                       eps, out_dt);
     VX_HIP(hipGetLastError());
     return 0;
 }
@@ -678,8 +792,42 @@ int qk_rope_scatter_launch(const uint16_t *qkv, const uint16_t *qn, const uint16
                            const uint32_t *pages, const uint32_t *slots, uint16_t *qout,
                            uint16_t *kp, uint16_t *vp, int64_t rows, int HQ, int HK, int D, int ps,
                            float eps, int kv_dt, hipStream_t st) {
-    hipLaunchKernelGGL(qk_rope_scatter_kernel, dim3((unsigned)rows), dim3(256), 0, st, qkv, qn, kn, cos_t,
-                       sin_t, pos, pages, slots, qout, kp, vp, HQ, HK, D, ps, eps, kv_dt);
+    if (D > 256 || D % 2 != 0) return set_error("qk_rope_scatter: head_dim must be even and <= 256");
+    if (rows == 0) return 0;
+    const int64_t waves = rows * (HQ + 2 * HK);
+    hipLaunchKernelGGL(qk_rope_scatter_kernel<false>, dim3((unsigned)vx_cdiv(waves, 4)), dim3(256), 0, st, qkv,
+                       nullptr, 0, qn, kn, cos_t, sin_t, pos, pages, slots, qout, kp, vp, (int)rows, HQ, HK, D,
+                       ps, eps, kv_dt);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+// q/k norm + RoPE + KV write straight from the qkv projection's split partials.
+int qkv_partial_rope_scatter_launch(const float *partial, int splits, const uint16_t *qn, const uint16_t *kn,
+                                    const uint16_t *cos_t, const uint16_t *sin_t, const uint32_t *pos,
+                                    const uint32_t *pages, const uint32_t *slots, uint16_t *qout, uint16_t *kp,
+                                    uint16_t *vp, int64_t rows, int HQ, int HK, int D, int ps, float eps, int kv_dt,
+                                    hipStream_t st) {
+    if (D > 256 || D % 2 != 0) return set_error("qk_rope_scatter: head_dim must be even and <= 256");
+    if (splits < 1 || splits > kMaxFusedSplits) return set_error("qk_rope_scatter: split count out of range");
+    if (rows == 0) return 0;
+    const int64_t waves = rows * (HQ + 2 * HK);
+    hipLaunchKernelGGL(qk_rope_scatter_kernel<true>, dim3((unsigned)vx_cdiv(waves, 4)), dim3(256), 0, st, nullptr,
+                       partial, splits, qn, kn, cos_t, sin_t, pos, pages, slots, qout, kp, vp, (int)rows, HQ, HK,
+                       D, ps, eps, kv_dt);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+// h += finish(partials) (bf16 residual), then y = RMSNorm(h) * ln when ln != null.
+int residual_rmsnorm_launch(const float *partial, int splits, float acc_scale, uint16_t *h, const uint16_t *ln,
+                            uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st) {
+    if (H % 8 != 0 || H > 8 * 1024) return set_error("rmsnorm: hidden size must be a multiple of 8 and <= 8192");
+    if (splits < 1 || splits > kMaxFusedSplits) return set_error("residual_rmsnorm: split count out of range");
+    if (rows == 0) return 0;
+    const unsigned threads = (unsigned)vx_cdiv(H / 8, 64) * 64;
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3((unsigned)rows), dim3(threads), 0, st, partial, splits,
+                       acc_scale, h, ln, y, (int)rows, (int)H, eps, out_dt);
     VX_HIP(hipGetLastError());
     return 0;
 }

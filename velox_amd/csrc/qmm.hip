@@ -51,6 +51,10 @@ constexpr size_t kMaxPartialBytes = (size_t)96 << 20;
 // by 32 (scale, bias) f16 pairs (row r, group half h at index 2r + h).  Tiles
 // are contiguous over their steps, so a wave streams contiguous memory.
 constexpr int kPackBlock = 1152;
+// Internal epilogue: raw f32 split partials [splits][M][N] (also for one
+// split); the consumer kernel reduces them in split order and finishes.
+constexpr int kEpiPartial = 100;
+constexpr int kMaxPartialSplits = 8;  // what the fused consumers read
 
 struct QmmArgs {
     const void *x;
@@ -189,7 +193,7 @@ __device__ __forceinline__ void epi_swiglu(const QmmArgs &a, int row, int f, flo
 template <int MT, int NT>
 __device__ __forceinline__ void store_acc(const QmmArgs &a, const floatx4 (&acc)[MT][NT], int m0, int col0,
                                           int sp, int kq) {
-    if (a.splits > 1) {
+    if (a.splits > 1 || a.epi == kEpiPartial) {
 #pragma unroll
         for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -684,7 +688,7 @@ int env_int(const char *name, int dflt) {
 
 // Prefetch depth of the streaming kernel by row-tile count: the register ring
 // holds P+1 steps of weights and activations.
-constexpr int stream_depth(int mt) { return mt == 1 ? 4 : (mt == 2 ? 3 : 2); }
+constexpr int stream_depth(int mt) { return mt <= 2 ? 4 : 3; }
 
 Plan make_plan(int64_t M, int64_t N, int64_t K, int epi, bool stream) {
     Plan p{};
@@ -696,8 +700,8 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int epi, bool stream) {
     const int target = 2 * cus;
     if (stream) {
         const int S = (int)(K / 128);
-        int nt = p.MT >= 3 ? 4 : 2;
-        if (epi == VX_EPI_SWIGLU) nt = std::max(nt, 2);
+        int nt = 2;
+        if (epi == kEpiPartial) nt = N >= 16384 ? 2 : 1;
         while (nt > (epi == VX_EPI_SWIGLU ? 2 : 1) && vx_cdiv(N, kWaves * nt * 16) * p.m_blocks * 4 < target)
             nt /= 2;
         nt = env_int("VX_QMM_NT", nt);
@@ -705,7 +709,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int epi, bool stream) {
         p.P = stream_depth(p.MT);
         p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 16);
         const int items = p.col_blocks * p.m_blocks;
-        int splits = std::max(1, target / std::max(1, items));
+        // partial mode: the consumer reads every split, so aim for fewer,
+        // longer workgroups (~0.7 per CU); otherwise ~2 per CU
+        int splits = epi == kEpiPartial ? std::max(1, std::min(kMaxPartialSplits, (int)((0.7 * cus) / std::max(1, items) + 0.5)))
+                                        : std::max(1, target / std::max(1, items));
         splits = env_int("VX_QMM_SPLITS", splits);
         splits = std::max(1, std::min(splits, S));
         int sps = (int)vx_cdiv(S, splits);
@@ -746,12 +753,12 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int epi, bool stream) {
     }
     p.total_items = p.col_blocks * p.splits;
     p.per_xcd = (int)vx_cdiv(p.total_items, 8);
-    p.partial_bytes = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
+    p.partial_bytes = (p.splits > 1 || epi == kEpiPartial) ? (size_t)p.splits * M * N * 4 : 0;
     return p;
 }
 
 void launch_reduce(const QmmArgs &a, const Plan &p, hipStream_t st) {
-    if (p.splits > 1) {
+    if (p.splits > 1 && a.epi != kEpiPartial) {
         const int64_t outs = (int64_t)a.M * (a.epi == VX_EPI_SWIGLU ? a.N / 2 : a.N);
         hipLaunchKernelGGL(qmm_reduce_kernel, dim3((unsigned)vx_cdiv(outs, 256)), dim3(256), 0, st, a);
     }
@@ -829,7 +836,7 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
     if (epi == VX_EPI_SWIGLU && (N % 32 != 0 || p.NT % 2 != 0))
         return set_error("qmm swiglu: N must be a multiple of 32 with paired tiles");
     void *ws = workspace;
-    if (p.splits > 1) {
+    if (p.partial_bytes > 0) {
         if (!ws) {
             VX_TRY(stream_workspace(st, kCounterBytes + p.partial_bytes, &ws));
         } else if (ws_bytes < kCounterBytes + p.partial_bytes) {
@@ -898,6 +905,25 @@ int qmm_packed(const void *x, const void *packed, void *y, const void *resid, in
     if (((uintptr_t)x % 16) != 0 || ((uintptr_t)packed % 16) != 0) return set_error("qmm packed: misaligned operand");
     return qmm_launch(x, (const uint32_t *)packed, nullptr, nullptr, y, resid, M, N, K, VX_F16, x_shift, y_shift,
                       round_dt, y_dt, epi, workspace, ws_bytes, st, true);
+}
+
+// Packed GEMM whose epilogue writes raw f32 split partials into the
+// workspace (after its reserved head): partial[(sp * M + row) * N + col] for
+// sp < *splits.  A fused consumer reduces them in split order.
+size_t qmm_partial_ws_bytes(int64_t M, int64_t N, int64_t K) {
+    if (K % 128 != 0) return kCounterBytes;
+    return kCounterBytes + make_plan(M, N, K, kEpiPartial, true).partial_bytes;
+}
+int qmm_packed_partial(const void *x, const void *packed, int64_t M, int64_t N, int64_t K, void *workspace,
+                       size_t ws_bytes, int *splits, const float **partial, hipStream_t st) {
+    if (N % 16 != 0 || K % 128 != 0) return set_error("qmm packed: N must be a multiple of 16 and K of 128");
+    if (((uintptr_t)x % 16) != 0 || ((uintptr_t)packed % 16) != 0) return set_error("qmm packed: misaligned operand");
+    if (!workspace) return set_error("qmm packed partial: needs a workspace");
+    const Plan p = make_plan(M, N, K, kEpiPartial, true);
+    *splits = p.splits;
+    *partial = (const float *)((const char *)workspace + kCounterBytes);
+    return qmm_launch(x, (const uint32_t *)packed, nullptr, nullptr, nullptr, nullptr, M, N, K, VX_F16, 0, 0,
+                      VX_BF16, VX_BF16, kEpiPartial, workspace, ws_bytes, st, true);
 }
 
 }  // namespace vx
