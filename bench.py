@@ -32,6 +32,9 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
 METRIC = "accepted tok/s, Qwen3-4B-shape int4 k=4 batch 16; verify-step HBM GB/s"
+# HBM bytes per verify GEMM op measured with rocprofv3 --pmc FETCH_SIZE /
+# WRITE_SIZE over this bench, scaled by a calibration copy (see the file)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_verify_gemm_qwen3_4b_b16_k4.json")
 
 
 def log(*a):
@@ -82,12 +85,30 @@ def cpu_baseline(cfg, weights, batch, k, threads):
                        f"({t_layer:.2f} s) = {t_full:.1f} s per full round")}
 
 
+def traffic_per_op():
+    """HBM bytes per verify GEMM op from the committed rocprofv3 --pmc summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["bytes_per_op"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def run_spec(args):
     import torch
 
     from velox_amd import engine, synth
 
     torch.cuda.set_device(0)
+    if args.calib_copy:
+        # one device copy of known size: the counter calibration of the --pmc runs
+        nb = args.calib_copy << 20
+        src = torch.ones(nb, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy of {nb} bytes done")
+        del src, dst
     B, k = args.batch, args.k
     cfg = synth.qwen3_config("qwen3-4b", max_pos=8192)
     t0 = time.time()
@@ -130,12 +151,15 @@ def run_spec(args):
         e.step_batch(states, k)
         profs.append(e.last_profile())
     e.set_profiling(False)
-    agg = {key: float(np.mean([p[key] for p in profs])) for key in profs[0]}
-    log("[bench] profile " + json.dumps({kk: round(v, 4) for kk, v in agg.items()}))
-    qmm_gbs = agg["verify_qmm_bytes"] / (agg["verify_qmm_ms"] * 1e-3) / 1e9
-    verify_bytes = agg["verify_qmm_bytes"] + agg["verify_attention_bytes"]
-    verify_gbs = verify_bytes / (agg["verify_ms"] * 1e-3) / 1e9
     ctx = states[0].kv_len
+    if profs:
+        agg = {key: float(np.mean([p[key] for p in profs])) for key in profs[0]}
+        log("[bench] profile " + json.dumps({kk: round(v, 4) for kk, v in agg.items()}))
+        qmm_gbs = agg["verify_qmm_bytes"] / (agg["verify_qmm_ms"] * 1e-3) / 1e9
+        verify_bytes = agg["verify_qmm_bytes"] + agg["verify_attention_bytes"]
+        verify_gbs = verify_bytes / (agg["verify_ms"] * 1e-3) / 1e9
+    else:  # no profiled rounds (e.g. under a profiler): no live kernel figures
+        agg, qmm_gbs, verify_bytes, verify_gbs = None, None, None, None
     res = {
         "metric": METRIC,
         "value": committed / elapsed,
@@ -153,15 +177,21 @@ def run_spec(args):
                    "global_batch": B, "k": k, "prompt_len": args.prompt, "context_at_end": ctx,
                    "seq_len": ctx, "parallelism": "single GPU"},
         "acceptance_rate": accepted / (args.steps * B * k),
-        "verify_step": {"ms": agg["verify_ms"], "algorithmic_bytes": verify_bytes, "hbm_gbs": verify_gbs,
-                        "draft_ms": agg["draft_ms"], "accept_ms": agg["accept_ms"]},
-        "roofline": {"bound": "hbm", "kernel": "qmm_int4_kernel (verify GEMMs, all shapes of one step)",
-                     "achieved": qmm_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": qmm_gbs / PEAK_HBM_GBS,
-                     "traffic": None,
-                     "launches_per_step": agg["verify_qmm_launches"],
-                     "avg_launch_us": agg["verify_qmm_ms"] * 1e3 / max(1, agg["verify_qmm_launches"]),
-                     "algorithmic_bytes_per_launch": agg["verify_qmm_bytes"] / max(1, agg["verify_qmm_launches"])},
-        "kernel_breakdown_ms": {kk: v for kk, v in agg.items() if kk.endswith("_ms")},
+        "verify_step": None if agg is None else {
+            "ms": agg["verify_ms"], "algorithmic_bytes": verify_bytes, "hbm_gbs": verify_gbs,
+            "draft_ms": agg["draft_ms"], "accept_ms": agg["accept_ms"]},
+        "roofline": {"bound": "hbm",
+                     "kernel": "qmm_f16_stream_kernel: the verify step's int4 GEMMs (36 layers x qkv, o, gate|up "
+                               "with its SwiGLU finish, down; plus the LM head), average per op",
+                     "achieved": qmm_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": None if qmm_gbs is None else qmm_gbs / PEAK_HBM_GBS,
+                     "traffic": traffic_per_op(),
+                     "launches_per_step": None if agg is None else agg["verify_qmm_launches"],
+                     "avg_launch_us": None if agg is None else
+                     agg["verify_qmm_ms"] * 1e3 / max(1, agg["verify_qmm_launches"]),
+                     "algorithmic_bytes_per_launch": None if agg is None else
+                     agg["verify_qmm_bytes"] / max(1, agg["verify_qmm_launches"])},
+        "kernel_breakdown_ms": None if agg is None else {kk: v for kk, v in agg.items() if kk.endswith("_ms")},
     }
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
@@ -225,6 +255,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--mode", choices=["spec", "qmm"], default="spec")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
+                    help="first do one device copy of MB MiB (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the verify path "

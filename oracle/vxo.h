@@ -17,9 +17,32 @@
  * result is rounded back to storage precision, as the reference does when a
  * candle op returns a tensor of dtype T.
  *
- * Parity status of each function (what pins it) is recorded in
- * oracle/README.md; functions with no independent check say
- * "parity unpinned" there.
+ * Parity status (what pins each function; tests/test_oracle*.py):
+ *   f32/f16/bf16 rounding     closed form vs numpy casts (test_round_to_dtypes)
+ *   philox4x32_10, u01        Random123 known answers + rocRAND fixture
+ *                             (test_philox_*), uniform layout (test_uniforms_layout)
+ *   expf                      <= 2 ulp of libm double (test_deterministic_exp_accuracy)
+ *   pack/unpack int4          dyn_quant.rs:205-218 known answer (test_pack_known_answer)
+ *   qmm_4bit                  dense X.deq(W)^T, group sizes + bias, all-zero codes
+ *                             (y = sum_g b_g sum x), one group, M=1 == row of M>1
+ *   paged_attention           dense softmax (causal, tree, window); shuffled block
+ *                             table invariance; chain tree == causal; kv_len 1 -> V
+ *   rope_tables / rope_apply  closed form (f32 argument) / complex rotation
+ *   kv_scatter                byte-exact copy
+ *   argmax, accept_greedy     spec.rs:271-301, :356-366 cases (first index, NaN)
+ *   row_softmax_stats, sample_residual, accept_stochastic, sample_draft
+ *                             p == q accepts everything; emitted tokens follow p
+ *                             (chi-square); no reference counterpart exists
+ *   accept_tree, tree_masks   brute-force walks on small trees
+ *   forward (model)           float64 dense Qwen3 (F32 oracle within 1e-4);
+ *                             batched == per sequence (bit-exact)
+ *   spec engine               spec greedy == target-only greedy; draft-KV hole
+ *                             quirk and fix; error and capacity cases
+ *   pages                     pages.rs:295-301 total_bytes, LIFO, all-or-nothing
+ *   rmsnorm, silu             formula pinned through the model checks above; the
+ *                             bf16 rounding points inside candle's RmsNorm / SiLU
+ *                             are "parity unpinned" (candle 0.10.2 is not in the
+ *                             reference tree and no reference test fixes them)
  */
 #ifndef VXO_H
 #define VXO_H

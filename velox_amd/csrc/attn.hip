@@ -171,42 +171,48 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     const int win = (int)a.window;
 
     for (int kb = k_lo + wave * kKeyBlock; kb < k_hi; kb += kAttnWaves * kKeyBlock) {
-        // ---- S^T for 64 keys: 4 tiles of 16 keys
-        floatx4 s[4][QT];
+        // ---- request K (4 tiles of 16 keys, lane = key within a tile) and V
+        // (lane = key) of the block together, so both round trips overlap
+        frag kf[4][DK];
 #pragma unroll
         for (int mt = 0; mt < 4; mt++) {
             const int key = kb + mt * 16 + lq;
             const int blk = min(key / a.ps, a.max_blocks - 1);
             const int page = min((int)btr[blk], a.num_pages - 1);
             const uint16_t *kr = (const uint16_t *)a.k + page * page_stride + hk * head_stride + (int64_t)(key % a.ps) * D;
-            frag kf[DK];
 #pragma unroll
-            for (int ks = 0; ks < DK; ks++) kf[ks] = __builtin_bit_cast(frag, *(const uint4 *)(kr + ks * 32 + lg * 8));
-#pragma unroll
-            for (int qt = 0; qt < QT; qt++) {
-                floatx4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < DK; ks++) c = MfmaT<KT>::mma(kf[ks], qf[qt][ks], c);
-                s[mt][qt] = c;
-            }
+            for (int ks = 0; ks < DK; ks++) kf[mt][ks] = __builtin_bit_cast(frag, *(const uint4 *)(kr + ks * 32 + lg * 8));
         }
-        // ---- stage V^T for the block (lane = key): vt[d][key]
+        uint4 vraw[D / 8];
         {
             const int key = kb + lane;
             const int blk = min(key / a.ps, a.max_blocks - 1);
             const int page = min((int)btr[blk], a.num_pages - 1);
             const uint16_t *vr = (const uint16_t *)a.v + page * page_stride + hk * head_stride + (int64_t)(key % a.ps) * D;
-            // the wave's own V^T tile: LDS operations of one wave complete in order
-            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int c = 0; c < D / 8; c++) {
-                uint4 raw = *(const uint4 *)(vr + c * 8);
-                const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+            for (int c = 0; c < D / 8; c++) vraw[c] = *(const uint4 *)(vr + c * 8);
+        }
+        // ---- S^T = K . Q^T
+        floatx4 s[4][QT];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    vt[(c * 8 + 2 * e) * VT_STRIDE + lane] = (uint16_t)(w4[e] & 0xffffu);
-                    vt[(c * 8 + 2 * e + 1) * VT_STRIDE + lane] = (uint16_t)(w4[e] >> 16);
-                }
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int qt = 0; qt < QT; qt++) {
+                floatx4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < DK; ks++) c = MfmaT<KT>::mma(kf[mt][ks], qf[qt][ks], c);
+                s[mt][qt] = c;
+            }
+        // ---- stage V^T for the block: vt[d][key]; the wave's own tile, and
+        // LDS operations of one wave complete in order
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int c = 0; c < D / 8; c++) {
+            const uint32_t w4[4] = {vraw[c].x, vraw[c].y, vraw[c].z, vraw[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                vt[(c * 8 + 2 * e) * VT_STRIDE + lane] = (uint16_t)(w4[e] & 0xffffu);
+                vt[(c * 8 + 2 * e + 1) * VT_STRIDE + lane] = (uint16_t)(w4[e] >> 16);
             }
         }
         // ---- mask, scale, block max

@@ -1,0 +1,137 @@
+"""Summaries of rocprofv3 result databases (ROCm 7.x writes SQLite).
+
+    python -m velox_amd.rocprof_summary trace RESULTS.db [--top N]
+        per (kernel, grid) dispatch count and duration statistics
+    python -m velox_amd.rocprof_summary verify RESULTS.db [--rounds R] [--pmc FILE.db ...]
+        the verify int4 GEMMs of the spec bench's timed rounds: every
+        qmm_f16_stream_kernel dispatch with an 80-row tile (<5, ...>) and a
+        one-row grid (prefill uses many row blocks), plus the SwiGLU finish
+        (qmm_reduce_kernel) that follows a gate|up dispatch; per-round sums
+        and the average per GEMM op, and with --pmc the FETCH_SIZE / WRITE_SIZE
+        sums of the same dispatches scaled by the calibration copy
+    python -m velox_amd.rocprof_summary calib RESULTS.db --bytes B
+        FETCH_SIZE or WRITE_SIZE (KiB) read for the largest
+        __amd_rocclr_copyBuffer dispatch, and the byte factor B / (KiB * 1024)
+
+The kernel-trace duration of a dispatch is end - start (ns).
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import re
+import sqlite3
+
+
+def _short(name: str) -> str:
+    n = name.replace("void ", "").replace("vx::", "").replace("(anonymous namespace)::", "")
+    return n.split("(")[0] if not n.startswith("(") else n
+
+
+def dispatches(db: str):
+    """[(short name, start, end, grid_x, grid_y, dispatch_id)] in start order."""
+    c = sqlite3.connect(db)
+    rows = c.execute("select name, start, end, grid_x, grid_y, dispatch_id from kernels order by start").fetchall()
+    return [(_short(n), s, e, gx, gy, d) for n, s, e, gx, gy, d in rows]
+
+
+def counters(db: str):
+    """{dispatch_id: {counter: value}} from a --pmc run."""
+    c = sqlite3.connect(db)
+    cols = [r[1] for r in c.execute("pragma table_info('counters_collection')")]
+    out = collections.defaultdict(dict)
+    for r in c.execute("select * from counters_collection"):
+        rec = dict(zip(cols, r))
+        out[rec["dispatch_id"]][rec["counter_name"]] = rec["value"]
+    return out
+
+
+def cmd_trace(args):
+    ds = dispatches(args.db)
+    st = collections.defaultdict(list)
+    for n, s, e, gx, gy, _ in ds:
+        st[(n, gx, gy)].append(e - s)
+    total = sum(e - s for _, s, e, *_ in ds)
+    print(f"total kernel time {total / 1e3:.1f} us over {len(ds)} dispatches")
+    print(f"{'kernel':64s} {'grid (wg x, y)':>14s} {'n':>6s} {'total us':>10s} {'avg us':>8s} {'med us':>8s} {'min us':>8s}")
+    for (n, gx, gy), v in sorted(st.items(), key=lambda kv: -sum(kv[1]))[: args.top]:
+        v.sort()
+        print(f"{n[:64]:64s} {f'{gx // 256}x{gy}':>14s} {len(v):6d} {sum(v) / 1e3:10.1f} {sum(v) / len(v) / 1e3:8.2f} "
+              f"{v[len(v) // 2] / 1e3:8.2f} {v[0] / 1e3:8.2f}")
+
+
+def _verify_ops(ds, rounds):
+    """Group the verify GEMM dispatches of the last `rounds` rounds into ops."""
+    ops = []
+    prev_gate_up = False
+    for n, s, e, gx, gy, d in ds:
+        m = re.match(r"qmm_f16_stream_kernel<(\d+), (\d+), (\d+), (true|false)>", n)
+        if m and m.group(1) == "5" and gy == 1:
+            ops.append([(n, s, e, d)])
+            prev_gate_up = True
+            continue
+        if n.startswith("qmm_reduce_kernel") and prev_gate_up and ops:
+            ops[-1].append((n, s, e, d))
+        prev_gate_up = False
+    return ops
+
+
+def cmd_verify(args):
+    ds = dispatches(args.db)
+    ops = _verify_ops(ds, args.rounds)
+    per_round = len(ops) // max(1, args.total_rounds)
+    sel = ops[-per_round * args.rounds:] if per_round else ops
+    dur = [sum(e - s for _, s, e, _ in op) for op in sel]
+    print(f"verify GEMM ops found: {len(ops)} ({per_round} per round over {args.total_rounds} rounds); "
+          f"summarised: last {args.rounds} rounds = {len(sel)} ops")
+    print(f"sum per round {sum(dur) / args.rounds / 1e3:.1f} us; average per op {sum(dur) / len(dur) / 1e3:.2f} us")
+    for path in args.pmc or []:
+        pm = counters(path)
+        pds = dispatches(path)
+        pops = _verify_ops(pds, args.rounds)
+        psel = pops[-per_round * args.rounds:] if per_round else pops
+        tot = collections.Counter()
+        for op in psel:
+            for _, _, _, d in op:
+                for k, v in pm.get(d, {}).items():
+                    tot[k] += v
+        for k, v in tot.items():
+            print(f"{path}: {k} summed over {len(psel)} ops = {v:.0f} KiB; per op {v / len(psel):.1f} KiB")
+
+
+def cmd_calib(args):
+    pm = counters(args.db)
+    ds = [d for d in dispatches(args.db) if d[0].startswith("__amd_rocclr_copyBuffer")]
+    best = None
+    for n, s, e, gx, gy, d in ds:
+        for k, v in pm.get(d, {}).items():
+            if best is None or v > best[1]:
+                best = (k, v, d)
+    if best is None:
+        print("no copy dispatch with counters found")
+        return
+    k, v, d = best
+    print(f"{k} of the calibration copy (dispatch {d}): {v:.0f} KiB for {args.bytes} bytes; "
+          f"factor = {args.bytes / (v * 1024):.4f}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    a = sub.add_parser("trace")
+    a.add_argument("db")
+    a.add_argument("--top", type=int, default=40)
+    b = sub.add_parser("verify")
+    b.add_argument("db")
+    b.add_argument("--rounds", type=int, default=4)
+    b.add_argument("--total-rounds", type=int, default=6)
+    b.add_argument("--pmc", nargs="*")
+    c = sub.add_parser("calib")
+    c.add_argument("db")
+    c.add_argument("--bytes", type=float, required=True)
+    args = ap.parse_args()
+    {"trace": cmd_trace, "verify": cmd_verify, "calib": cmd_calib}[args.cmd](args)
+
+
+if __name__ == "__main__":
+    main()
