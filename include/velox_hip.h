@@ -66,11 +66,13 @@ size_t vx_qmm_workspace_size(int64_t m, int64_t n, int64_t k);
 
 /* Packed weights for the verify path (no reference counterpart: the
  * reference's Metal kernel reads MLX's row-major words, metal_kernels.rs
- * :418-479; the packed form holds the same values).  Per 16-row tile and
- * 128-wide k step, one 1152-byte block: 1024 bytes of nibbles in MFMA lane
- * order, then 32 (scale, bias) f16 pairs.  N % 16 == 0, K % 128 == 0, group
- * size 64.  vx_qmm_pack_4bit converts device MLX tensors on `stream`;
- * vx_qmm_4bit_packed is vx_qmm_4bit_ex over packed weights. */
+ * :418-479; the packed form holds the same values).  Per 32-row tile and
+ * 128-wide k step, one 2304-byte block laid out for the 32x32x16 MFMA B
+ * operand: 2048 bytes of nibbles (lane L: row L%32, k 16j + 8*(L/32) .. +7
+ * for j < 8), then (scale, bias) of the step's two groups per row as f16.
+ * N % 32 == 0, K % 128 == 0, group size 64.  vx_qmm_pack_4bit converts
+ * device MLX tensors on `stream`; vx_qmm_4bit_packed is vx_qmm_4bit_ex over
+ * packed weights (X 16-byte aligned). */
 size_t vx_qmm_packed_size(int64_t n, int64_t k);
 int vx_qmm_pack_4bit(const uint32_t *qweight, const void *scales, const void *biases, void *packed,
                      int64_t n, int64_t k, void *stream);

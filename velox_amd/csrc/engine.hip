@@ -93,7 +93,7 @@ int qmm_pack(const uint32_t *w, const void *s, const void *b, void *out, int64_t
 int qmm_packed(const void *x, const void *packed, void *y, const void *resid, int64_t M, int64_t N, int64_t K,
                int x_shift, int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
                hipStream_t st);
-size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi);
+size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi, bool packed);
 size_t attn_workspace_bytes(int64_t n_seqs, int64_t h_kv, int64_t n_qtiles, int64_t n_splits, int64_t D);
 int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool, const uint32_t *bt,
                            const uint32_t *cu, const uint32_t *kvo, const uint64_t *tmask, void *out,
@@ -491,7 +491,7 @@ extern "C" int vx_model_create(const vx_qwen3_config *cfg, const vx_weights_host
     VX_REQUIRE(H <= 8192, "model: hidden size above 8192 is not supported");
     VX_REQUIRE(D % 32 == 0 && D <= 256, "model: head_dim must be a multiple of 32 and <= 256");
     VX_REQUIRE(F % 16 == 0, "model: intermediate size must be a multiple of 16");
-    VX_REQUIRE(cfg->vocab % 16 == 0, "model: vocab must be a multiple of 16");
+    VX_REQUIRE(cfg->vocab % 32 == 0, "model: vocab must be a multiple of 32");
     auto m = std::make_unique<vx_model>();
     m->cfg = *cfg;
     m->L = L;
@@ -652,9 +652,9 @@ size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int
     size_t need = 0;
     need = std::max(need, qmm_partial_ws_bytes(rows, QW + 2 * KW, H));
     need = std::max(need, qmm_partial_ws_bytes(rows, H, QW));
-    need = std::max(need, qmm_workspace_bytes(rows, 2 * F, H, VX_EPI_SWIGLU));
+    need = std::max(need, qmm_workspace_bytes(rows, 2 * F, H, VX_EPI_SWIGLU, true));
     need = std::max(need, qmm_partial_ws_bytes(rows, H, F));
-    need = std::max(need, qmm_workspace_bytes(logit_rows, c.vocab, H, VX_EPI_STORE));
+    need = std::max(need, qmm_workspace_bytes(logit_rows, c.vocab, H, VX_EPI_STORE, true));
     // attention: upper bound on its split plan (see paged_attention_launch)
     const int64_t G = c.n_heads / c.n_kv_heads;
     const int64_t qn_max = c.head_dim <= 128 ? 64 : 32;

@@ -44,13 +44,16 @@ constexpr int kWaves = 4;
 constexpr int kChunkGroups = 4;          // groups of 64 staged per LDS chunk
 constexpr size_t kCounterBytes = 65536;  // reserved head of the workspace (kept zero)
 constexpr size_t kMaxPartialBytes = (size_t)96 << 20;
-// Packed weight layout of the streaming kernel: per 16-row tile and 128-wide
-// k step one block of 1024 bytes of nibbles in MFMA lane order (lane L: row
-// L%16 of the tile, k 32*(L/16) .. +31 of the step, four words; inside a word
-// the nibbles of k0..k7 sit at positions 0,4,1,5,2,6,3,7) followed
-// by 32 (scale, bias) f16 pairs (row r, group half h at index 2r + h).  Tiles
-// are contiguous over their steps, so a wave streams contiguous memory.
-constexpr int kPackBlock = 1152;
+// Packed weight layout (the engine's): per 32-row tile and 128-wide k step one
+// block of kPackBlock bytes, tiles contiguous over their steps so a wave
+// streams contiguous memory.  Lane L of a v_mfma_f32_32x32x16 B operand holds
+// row L%32 of the tile and, for MFMA j (j < 8) of the step, the 8 k values
+// 16j + 8*(L/32) .. +7: one word, with the nibbles of k0..k7 at positions
+// 0,4,1,5,2,6,3,7 (the order dequant8 emits).  Bytes [0, 1024): words 0..3 of
+// every lane (16 bytes at 16 L); [1024, 2048): words 4..7; [2048, 2304): per
+// row r, at 2048 + 8r, (scale, bias) of the step's two groups as f16
+// (s0, b0, s1, b1).  Words 0..3 belong to the first group, 4..7 to the second.
+constexpr int kPackBlock = 2304;
 // Internal epilogue: raw f32 split partials [splits][M][N] (also for one
 // split); the consumer kernel reduces them in split order and finishes.
 constexpr int kEpiPartial = 100;
@@ -419,7 +422,7 @@ __global__ __launch_bounds__(256) void qmm_int4_kernel(QmmArgs a) {
 // step loop is unrolled by the ring size so every slot is a fixed register
 // set); the activations of step s+1 move to the other LDS buffer after the
 // MFMAs of step s, one barrier per step.
-template <int MT, int NT, int P, bool PACKED>
+template <int MT, int NT, int P>
 __global__ __launch_bounds__(256) void qmm_f16_stream_kernel(QmmArgs a) {
     constexpr int R = P + 1;
     static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
@@ -457,28 +460,17 @@ __global__ __launch_bounds__(256) void qmm_f16_stream_kernel(QmmArgs a) {
     }
     // MLX layout: weight row col, words 16 st + 4 kq .. +3; scales/biases
     // [N, G] (the pair of groups of step st is one 32-bit word).
-    // Packed layout: block (tile, st) of kPackBlock bytes, this lane's 16
-    // bytes at lane*16 and its (scale, bias) pair at 1024 + 4 (2 (lane%16) + kq/2).
     const uint4 *wrow[NT];
     const uint32_t *srow[NT], *brow[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        if constexpr (PACKED) {
-            const int tile = min(col0 / 16 + nt, a.N / 16 - 1);
-            const uint8_t *blk = (const uint8_t *)a.w + (int64_t)tile * a.S * kPackBlock;
-            wrow[nt] = (const uint4 *)blk + lane;
-            srow[nt] = (const uint32_t *)(blk + 1024) + 2 * (lane & 15) + (kq >> 1);
-            brow[nt] = nullptr;
-        } else {
-            const int col = min(col0 + nt * 16, a.N - 1);
-            wrow[nt] = (const uint4 *)(a.w + (int64_t)col * (a.K / 8)) + kq;
-            srow[nt] = (const uint32_t *)(a.s + (int64_t)col * a.G);
-            brow[nt] = (const uint32_t *)(a.b + (int64_t)col * a.G);
-        }
+        const int col = min(col0 + nt * 16, a.N - 1);
+        wrow[nt] = (const uint4 *)(a.w + (int64_t)col * (a.K / 8)) + kq;
+        srow[nt] = (const uint32_t *)(a.s + (int64_t)col * a.G);
+        brow[nt] = (const uint32_t *)(a.b + (int64_t)col * a.G);
     }
-    // byte selectors replicating one 16-bit half of a word into both halves
+    // byte selector replicating the lane's group half (kq/2) into both halves
     const uint32_t hsel = (kq & 2) ? 0x03020302u : 0x01000100u;
-    constexpr uint32_t kLoHalf = 0x01000100u, kHiHalf = 0x03020302u;
     const DqConst dq = dq_const();
 
     floatx4 acc[MT][NT];
@@ -496,22 +488,15 @@ __global__ __launch_bounds__(256) void qmm_f16_stream_kernel(QmmArgs a) {
         for (int i = 0; i < UPT; i++) xv[i] = *(const uint4 *)(xh + xoff[i] + st * 128);
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            if constexpr (PACKED) {
-                w[nt] = wrow[nt][st * (kPackBlock / 16)];
-                sv[nt] = srow[nt][st * (kPackBlock / 4)];
-                bv[nt] = 0u;
-            } else {
-                w[nt] = wrow[nt][st * 4];
-                sv[nt] = srow[nt][st];
-                bv[nt] = brow[nt][st];
-            }
+            w[nt] = wrow[nt][st * 4];
+            sv[nt] = srow[nt][st];
+            bv[nt] = brow[nt][st];
         }
     };
-    // packed weights hold each word's nibbles in the order dequant8 emits
-    // them as k (natural order), so only the row-major path permutes X
+    // dequant8 emits the word's nibble pairs (k, k+4): permute X to match
     auto stage = [&](int buf, const uint4 (&xv)[UPT]) {
 #pragma unroll
-        for (int i = 0; i < UPT; i++) xs[buf][tid + 256 * i] = PACKED ? xv[i] : permute_k8(xv[i]);
+        for (int i = 0; i < UPT; i++) xs[buf][tid + 256 * i] = permute_k8(xv[i]);
     };
 
     // One step: request step st+P into its ring slot (clamped to the last
@@ -529,13 +514,8 @@ __global__ __launch_bounds__(256) void qmm_f16_stream_kernel(QmmArgs a) {
         half2_t s2[NT], b2[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            if constexpr (PACKED) {
-                s2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt], sr[I][nt], kLoHalf));
-                b2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt], sr[I][nt], kHiHalf));
-            } else {
-                s2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt], sr[I][nt], hsel));
-                b2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(br[I][nt], br[I][nt], hsel));
-            }
+            s2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt], sr[I][nt], hsel));
+            b2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(br[I][nt], br[I][nt], hsel));
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -592,7 +572,8 @@ __device__ __forceinline__ uint32_t pack_nibbles(uint32_t w) {
 }
 
 // MLX [N, K/8] words + [N, K/64] scales/biases -> packed blocks.  One
-// workgroup of 64 threads per (tile, step) block.
+// workgroup of 64 threads per (tile, step) block; thread L writes lane L's
+// two 16-byte pieces, threads < 32 also the scale/bias pairs of row L.
 __global__ __launch_bounds__(64) void qmm_pack_kernel(const uint32_t *w, const uint16_t *s, const uint16_t *b,
                                                       uint8_t *out, int N, int K) {
     const int S = K / 128, G = K / 64;
@@ -600,15 +581,229 @@ __global__ __launch_bounds__(64) void qmm_pack_kernel(const uint32_t *w, const u
     const int tile = (int)(blk / S), st = (int)(blk - (int64_t)tile * S);
     const int lane = threadIdx.x;
     uint8_t *o = out + blk * kPackBlock;
-    const int row = tile * 16 + (lane & 15);
-    const uint4 v = *(const uint4 *)(w + (int64_t)row * (K / 8) + st * 16 + 4 * (lane >> 4));
-    *(uint4 *)(o + lane * 16) = make_uint4(pack_nibbles(v.x), pack_nibbles(v.y), pack_nibbles(v.z), pack_nibbles(v.w));
+    const int row = tile * 32 + (lane & 31);
+    const int kh = lane >> 5;
+    const uint4 *src = (const uint4 *)(w + (int64_t)row * (K / 8) + st * 16);
+    const uint4 q0 = src[0], q1 = src[1], q2 = src[2], q3 = src[3];
+    const uint32_t words[16] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w,
+                                q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+    uint32_t pw[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) pw[j] = pack_nibbles(words[2 * j + kh]);
+    *(uint4 *)(o + lane * 16) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    *(uint4 *)(o + 1024 + lane * 16) = make_uint4(pw[4], pw[5], pw[6], pw[7]);
     if (lane < 32) {
-        const int r = tile * 16 + (lane >> 1);
-        const int g = 2 * st + (lane & 1);
-        const uint32_t pair = (uint32_t)s[(int64_t)r * G + g] | ((uint32_t)b[(int64_t)r * G + g] << 16);
-        *(uint32_t *)(o + 1024 + lane * 4) = pair;
+        const int64_t r = (int64_t)tile * 32 + lane;
+        const int g = 2 * st;
+        const uint32_t p0 = (uint32_t)s[r * G + g] | ((uint32_t)b[r * G + g] << 16);
+        const uint32_t p1 = (uint32_t)s[r * G + g + 1] | ((uint32_t)b[r * G + g + 1] << 16);
+        *(uint2 *)(o + 2048 + lane * 8) = make_uint2(p0, p1);
     }
+}
+
+// Writes a wave's v_mfma_f32_32x32x16 accumulators (lane L, element i: column
+// L%32, row 8*(i/4) + 4*(L/32) + i%4 of the 32x32 tile): split partials when
+// the K range is split or the caller asked for them, else the epilogue.
+// SwiGLU: a 32-column tile is gate rows [16T, 16T+16) then up rows of the same
+// features (weights interleaved in 16-row blocks), so lane L < 16 of each half
+// pairs with lane L + 16.
+template <int MT, int NT>
+__device__ __forceinline__ void store_acc32(const QmmArgs &a, const floatx16 (&acc)[MT][NT], int m0, int col0,
+                                            int sp, int lane) {
+    const int hr = 4 * (lane >> 5);
+    const int c = lane & 31;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            // the accumulators are only read with constant indices here; the
+            // per-element work below runs on this copy, so a loop the compiler
+            // keeps rolled cannot push the accumulators themselves to scratch
+            float v[16], u[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = acc[t][nt][i];
+            const int col = col0 + nt * 32;
+            if (a.splits > 1 || a.epi == kEpiPartial) {
+                if (col >= a.N) continue;
+                for (int i = 0; i < 16; i++) {
+                    const int row = m0 + 32 * t + 8 * (i >> 2) + hr + (i & 3);
+                    if (row < a.M) a.partial[((int64_t)sp * a.M + row) * a.N + col] = v[i];
+                }
+            } else if (a.epi == VX_EPI_SWIGLU) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) u[i] = __shfl_down(v[i], 16);
+                const int tile = (col0 - c) / 32 + nt;
+                const int f = tile * 16 + c;
+                if (c >= 16 || tile * 32 >= a.N) continue;
+                for (int i = 0; i < 16; i++) {
+                    const int row = m0 + 32 * t + 8 * (i >> 2) + hr + (i & 3);
+                    if (row < a.M) epi_swiglu(a, row, f, v[i], u[i]);
+                }
+            } else {
+                if (col >= a.N) continue;
+                for (int i = 0; i < 16; i++) {
+                    const int row = m0 + 32 * t + 8 * (i >> 2) + hr + (i & 3);
+                    if (row < a.M) epi_elem(a, row, col, v[i]);
+                }
+            }
+        }
+}
+
+// GEMM over packed weights on v_mfma_f32_32x32x16_f16 (the engine's path).
+// A workgroup is four waves; a wave owns NT tiles of 32 output columns and
+// MT tiles of 32 rows.  K advances in 128-wide steps: per step a lane loads
+// two 16-byte weight pieces and one (scale, bias) word pair per tile (the
+// eight words feed the step's eight MFMAs), and the workgroup stages the
+// step's activations in LDS in A-fragment order (lane L: row L%32, k
+// 16j + 8*(L/32) .. +7, 16 contiguous bytes, no permute: the packed nibble
+// order already yields natural k).  Weights, scales and activations of step
+// s+P are requested before step s computes, in a ring of P+1 register slots
+// (fixed slots, unconditional clamped loads, the requests pinned at the head
+// of the step so the compiler's wait counts stay exact); one barrier per step.
+template <int MT, int NT, int P>
+__global__ __launch_bounds__(256) void qmm_f16_p32_kernel(QmmArgs a) {
+    constexpr int R = P + 1;
+    static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
+    constexpr int FR = 8 * MT;       // activation fragments (j, t) per step
+    constexpr int UPT = FR * 64 / 256;  // 16-byte pieces per thread per step
+    __shared__ uint4 xs[2][FR * 64];
+
+    const int bid = blockIdx.x;
+    const int item = (bid & 7) * a.per_xcd + (bid >> 3);
+    if (item >= a.total_items) return;
+    const int cb = item / a.splits;
+    const int sp = item - cb * a.splits;
+    const int m0 = blockIdx.y * MT * 32;
+    const int s_lo = sp * a.sps;
+    const int s_hi = min(a.S, s_lo + a.sps);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col0 = cb * (kWaves * NT * 32) + wave * NT * 32 + (lane & 31);
+
+    // activation pieces: unit u = tid + 256 i is fragment (j, t) = divmod(u / 64, MT), lane u % 64;
+    // rows past M re-read row M-1 (finite values whose results are never stored)
+    const uint16_t *xh = (const uint16_t *)a.x;
+    int xoff[UPT];
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + 256 * i;
+        const int ln = u & 63;
+        const int jt = u >> 6;
+        const int j = jt / MT;
+        const int t = jt - j * MT;
+        const int row = min(m0 + 32 * t + (ln & 31), a.M - 1);
+        xoff[i] = row * a.K + 16 * j + 8 * (ln >> 5);
+    }
+    const uint8_t *wblk[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tile = min(col0 / 32 + nt, a.N / 32 - 1);
+        wblk[nt] = (const uint8_t *)a.w + (int64_t)tile * a.S * kPackBlock;
+    }
+    constexpr uint32_t kLoHalf = 0x01000100u, kHiHalf = 0x03020302u;
+    const DqConst dq = dq_const();
+
+    floatx16 acc[MT][NT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[t][nt][i] = 0.f;
+
+    uint4 wlo[R][NT], whi[R][NT];  // words 0..3 / 4..7 of each tile
+    uint2 sr[R][NT];
+    uint4 xr[R][UPT];
+
+    auto issue = [&](int st, uint4 (&w0)[NT], uint4 (&w1)[NT], uint2 (&sv)[NT], uint4 (&xv)[UPT]) {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) xv[i] = *(const uint4 *)(xh + xoff[i] + st * 128);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const uint8_t *bp = wblk[nt] + (int64_t)st * kPackBlock;
+            w0[nt] = *(const uint4 *)(bp + lane * 16);
+            w1[nt] = *(const uint4 *)(bp + 1024 + lane * 16);
+            sv[nt] = *(const uint2 *)(bp + 2048 + (lane & 31) * 8);
+        }
+    };
+    // component-wise copy: a whole-struct copy becomes a memcpy that keeps the
+    // register ring in scratch memory
+    auto stage = [&](int buf, const uint4 (&xv)[UPT]) {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) xs[buf][tid + 256 * i] = make_uint4(xv[i].x, xv[i].y, xv[i].z, xv[i].w);
+    };
+    auto step = [&](int st, auto slot_c) {
+        constexpr int I = decltype(slot_c)::value;
+        constexpr int NX = (I + P) % R;
+        issue(min(st + P, s_hi - 1), wlo[NX], whi[NX], sr[NX], xr[NX]);
+        // keep the prefetch at the head of the step: if the scheduler sinks it
+        // below the MFMAs, consuming an older slot waits for every load in flight
+        __builtin_amdgcn_sched_barrier(0);
+        const int buf = (st - s_lo) & 1;
+        half2_t s2[NT][2], b2[NT][2];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            s2[nt][0] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].x, sr[I][nt].x, kLoHalf));
+            b2[nt][0] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].x, sr[I][nt].x, kHiHalf));
+            s2[nt][1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].y, sr[I][nt].y, kLoHalf));
+            b2[nt][1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].y, sr[I][nt].y, kHiHalf));
+        }
+        // sub-step j+1's A fragments are read from LDS before the MFMAs of
+        // sub-step j are issued (a scheduling barrier keeps the compiler from
+        // sinking the reads next to their use), so the MFMAs cover the LDS
+        // latency; the dequant of j+1 interleaves with those MFMAs
+        half8_t af[2][MT], bq[2][NT];
+        auto lds_a = [&](int j, int c) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) af[c][t] = __builtin_bit_cast(half8_t, xs[buf][(j * MT + t) * 64 + lane]);
+        };
+        auto deq_b = [&](int j, int c) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint4 q = (j >> 2) ? whi[I][nt] : wlo[I][nt];
+                const uint32_t word = (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
+                bq[c][nt] = dequant8(word, s2[nt][j >> 2], b2[nt][j >> 2], dq);
+            }
+        };
+        lds_a(0, 0);
+        deq_b(0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j < 7) lds_a(j + 1, (j + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (j < 7) deq_b(j + 1, (j + 1) & 1);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][t], bq[j & 1][nt], acc[t][nt], 0, 0, 0);
+        }
+        stage(buf ^ 1, xr[(I + 1) % R]);  // past the last step this stages a copy nobody reads
+        __syncthreads();
+    };
+
+#pragma unroll
+    for (int i = 0; i < P; i++) issue(min(s_lo + i, s_hi - 1), wlo[i], whi[i], sr[i], xr[i]);
+    stage(0, xr[0]);
+    __syncthreads();
+
+    int st = s_lo;
+    for (; st + R <= s_hi; st += R) {
+        step(st + 0, std::integral_constant<int, 0>{});
+        if constexpr (R > 1) step(st + 1, std::integral_constant<int, 1 % R>{});
+        if constexpr (R > 2) step(st + 2, std::integral_constant<int, 2 % R>{});
+        if constexpr (R > 3) step(st + 3, std::integral_constant<int, 3 % R>{});
+        if constexpr (R > 4) step(st + 4, std::integral_constant<int, 4 % R>{});
+        if constexpr (R > 5) step(st + 5, std::integral_constant<int, 5 % R>{});
+    }
+    // tail: fewer than R steps remain; slot of step st + i is i
+    if (st < s_hi) step(st, std::integral_constant<int, 0>{});
+    if constexpr (R > 2) if (st + 1 < s_hi) step(st + 1, std::integral_constant<int, 1 % R>{});
+    if constexpr (R > 3) if (st + 2 < s_hi) step(st + 2, std::integral_constant<int, 2 % R>{});
+    if constexpr (R > 4) if (st + 3 < s_hi) step(st + 3, std::integral_constant<int, 3 % R>{});
+    if constexpr (R > 5) if (st + 4 < s_hi) step(st + 4, std::integral_constant<int, 4 % R>{});
+    store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
 }
 
 // Split-K finish: sum the partials of each output in split order, then the
@@ -677,6 +872,7 @@ __global__ void add_bias_kernel(void *y, const void *bias, int64_t m, int64_t n)
 
 struct Plan {
     bool stream;  // f16 streaming kernel (else the LDS-chunked kernel)
+    bool p32;     // packed weights on the 32x32 MFMA kernel
     int MT, NT, P, splits, gps, sps, col_blocks, m_blocks, per_xcd, total_items;
     size_t partial_bytes;
 };
@@ -689,6 +885,46 @@ int env_int(const char *name, int dflt) {
 // Prefetch depth of the streaming kernel by row-tile count: the register ring
 // holds P+1 steps of weights and activations.
 constexpr int stream_depth(int mt) { return mt <= 2 ? 4 : 3; }
+
+// Prefetch depth of the packed kernel by tile counts (register budget).
+constexpr int p32_depth(int mt, int nt) { return mt == 1 ? 4 : (mt == 2 ? 3 : (nt == 1 ? 2 : 1)); }
+
+// Packed-weight plan: 32-row tiles (up to 3 per workgroup), 32-column tiles.
+Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
+    Plan p{};
+    p.stream = true;
+    p.p32 = true;
+    const int cus = device_cu_count();
+    p.MT = (int)std::min<int64_t>(3, std::max<int64_t>(1, vx_cdiv(std::min<int64_t>(M, 96), 32)));
+    p.m_blocks = (int)vx_cdiv(M, p.MT * 32);
+    const int S = (int)(K / 128);
+    int nt = env_int("VX_QMM_NT", 1);
+    p.NT = nt;
+    p.P = p32_depth(p.MT, nt);
+    p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 32);
+    const int items = p.col_blocks * p.m_blocks;
+    // three row tiles hold one workgroup per CU (registers); fewer hold two.
+    // Partial mode aims a little lower: its consumer reads every split.
+    const double per_cu = p.MT >= 3 ? 1.0 : 2.0;
+    const double target = per_cu * cus * (epi == kEpiPartial ? 0.9 : 1.0);
+    int splits = std::max(1, (int)(target / std::max(1, items) + 0.5));
+    if (epi == kEpiPartial) splits = std::min(splits, kMaxPartialSplits);
+    splits = env_int("VX_QMM_SPLITS", splits);
+    splits = std::max(1, std::min(splits, S));
+    int sps = (int)vx_cdiv(S, splits);
+    splits = (int)vx_cdiv(S, sps);
+    while (splits > 1 && (size_t)splits * M * N * 4 > kMaxPartialBytes) {
+        sps++;
+        splits = (int)vx_cdiv(S, sps);
+    }
+    p.splits = splits;
+    p.sps = sps;
+    p.gps = 2 * sps;
+    p.total_items = p.col_blocks * p.splits;
+    p.per_xcd = (int)vx_cdiv(p.total_items, 8);
+    p.partial_bytes = (p.splits > 1 || epi == kEpiPartial) ? (size_t)p.splits * M * N * 4 : 0;
+    return p;
+}
 
 Plan make_plan(int64_t M, int64_t N, int64_t K, int epi, bool stream) {
     Plan p{};
@@ -764,19 +1000,38 @@ void launch_reduce(const QmmArgs &a, const Plan &p, hipStream_t st) {
     }
 }
 
-template <int MT, int NT, bool PACKED>
+template <int MT, int NT>
 void launch_stream(const QmmArgs &a, const Plan &p, hipStream_t st) {
     dim3 grid(p.per_xcd * 8, p.m_blocks);
-    hipLaunchKernelGGL((qmm_f16_stream_kernel<MT, NT, stream_depth(MT), PACKED>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((qmm_f16_stream_kernel<MT, NT, stream_depth(MT)>), grid, dim3(256), 0, st, a);
     launch_reduce(a, p, st);
 }
 
-template <bool PACKED>
+template <int MT, int NT>
+void launch_p32(const QmmArgs &a, const Plan &p, hipStream_t st) {
+    dim3 grid(p.per_xcd * 8, p.m_blocks);
+    hipLaunchKernelGGL((qmm_f16_p32_kernel<MT, NT, p32_depth(MT, NT)>), grid, dim3(256), 0, st, a);
+    launch_reduce(a, p, st);
+}
+
+int dispatch_p32(const QmmArgs &a, const Plan &p, hipStream_t st) {
+#define VX_CASE(mt, nt)                \
+    if (p.MT == mt && p.NT == nt) {    \
+        launch_p32<mt, nt>(a, p, st);  \
+        return 0;                      \
+    }
+    VX_CASE(1, 1) VX_CASE(1, 2)
+    VX_CASE(2, 1) VX_CASE(2, 2)
+    VX_CASE(3, 1) VX_CASE(3, 2)
+#undef VX_CASE
+    return set_error("qmm: no packed kernel for tile plan");
+}
+
 int dispatch_stream(const QmmArgs &a, const Plan &p, hipStream_t st) {
-#define VX_CASE(mt, nt)                           \
-    if (p.MT == mt && p.NT == nt) {               \
-        launch_stream<mt, nt, PACKED>(a, p, st);  \
-        return 0;                                 \
+#define VX_CASE(mt, nt)                   \
+    if (p.MT == mt && p.NT == nt) {       \
+        launch_stream<mt, nt>(a, p, st);  \
+        return 0;                         \
     }
     VX_CASE(1, 1) VX_CASE(1, 2) VX_CASE(1, 4)
     VX_CASE(2, 1) VX_CASE(2, 2) VX_CASE(2, 4)
@@ -821,10 +1076,10 @@ bool fast_ok(int dt, int64_t K, int64_t gs, const void *x, const void *w, const 
 
 }  // namespace
 
-// Workspace of the f16 (streaming) path.
-size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi) {
+// Workspace of the f16 paths (row-major MLX weights, or packed weights).
+size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi, bool packed) {
     if (k % 128 != 0) return kCounterBytes;
-    Plan p = make_plan(m, n, k, epi, true);
+    Plan p = packed ? make_plan_p32(m, n, k, epi) : make_plan(m, n, k, epi, true);
     return kCounterBytes + p.partial_bytes;
 }
 
@@ -832,8 +1087,8 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
                const void *resid, int64_t M, int64_t N, int64_t K, int x_dt, int x_shift,
                int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
                hipStream_t st, bool packed = false) {
-    Plan p = make_plan(M, N, K, epi, x_dt == VX_F16);
-    if (epi == VX_EPI_SWIGLU && (N % 32 != 0 || p.NT % 2 != 0))
+    Plan p = packed ? make_plan_p32(M, N, K, epi) : make_plan(M, N, K, epi, x_dt == VX_F16);
+    if (epi == VX_EPI_SWIGLU && (N % 32 != 0 || (!p.p32 && p.NT % 2 != 0)))
         return set_error("qmm swiglu: N must be a multiple of 32 with paired tiles");
     void *ws = workspace;
     if (p.partial_bytes > 0) {
@@ -869,8 +1124,7 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
     a.acc_scale = ldexpf(1.0f, x_shift);
     a.store_scale = ldexpf(1.0f, -y_shift);
     if (!p.stream && x_dt != VX_BF16) return set_error("qmm: the chunked kernel takes bf16 activations only");
-    int rc = p.stream ? (packed ? dispatch_stream<true>(a, p, st) : dispatch_stream<false>(a, p, st))
-                      : dispatch_fast<true>(a, p, st);
+    int rc = p.p32 ? dispatch_p32(a, p, st) : (p.stream ? dispatch_stream(a, p, st) : dispatch_fast<true>(a, p, st));
     if (rc) return rc;
     VX_HIP(hipGetLastError());
     return 0;
@@ -883,12 +1137,12 @@ int qmm_fast(const void *x, const uint32_t *w, const void *s, const void *b, voi
                       ws_bytes, st);
 }
 
-size_t qmm_packed_bytes(int64_t n, int64_t k) { return (size_t)(n / 16) * (size_t)(k / 128) * kPackBlock; }
+size_t qmm_packed_bytes(int64_t n, int64_t k) { return (size_t)(n / 32) * (size_t)(k / 128) * kPackBlock; }
 
 int qmm_pack(const uint32_t *w, const void *s, const void *b, void *out, int64_t N, int64_t K, hipStream_t st) {
-    if (N % 16 != 0 || K % 128 != 0) return set_error("qmm pack: N must be a multiple of 16 and K of 128");
+    if (N % 32 != 0 || K % 128 != 0) return set_error("qmm pack: N must be a multiple of 32 and K of 128");
     if (((uintptr_t)w % 16) != 0 || ((uintptr_t)out % 16) != 0) return set_error("qmm pack: misaligned operand");
-    const int64_t blocks = (N / 16) * (K / 128);
+    const int64_t blocks = (N / 32) * (K / 128);
     if (blocks == 0) return 0;
     hipLaunchKernelGGL(qmm_pack_kernel, dim3((unsigned)blocks), dim3(64), 0, st, w, (const uint16_t *)s,
                        (const uint16_t *)b, (uint8_t *)out, (int)N, (int)K);
@@ -901,7 +1155,7 @@ int qmm_pack(const uint32_t *w, const void *s, const void *b, void *out, int64_t
 int qmm_packed(const void *x, const void *packed, void *y, const void *resid, int64_t M, int64_t N, int64_t K,
                int x_shift, int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
                hipStream_t st) {
-    if (N % 16 != 0 || K % 128 != 0) return set_error("qmm packed: N must be a multiple of 16 and K of 128");
+    if (N % 32 != 0 || K % 128 != 0) return set_error("qmm packed: N must be a multiple of 32 and K of 128");
     if (((uintptr_t)x % 16) != 0 || ((uintptr_t)packed % 16) != 0) return set_error("qmm packed: misaligned operand");
     return qmm_launch(x, (const uint32_t *)packed, nullptr, nullptr, y, resid, M, N, K, VX_F16, x_shift, y_shift,
                       round_dt, y_dt, epi, workspace, ws_bytes, st, true);
@@ -912,14 +1166,14 @@ int qmm_packed(const void *x, const void *packed, void *y, const void *resid, in
 // sp < *splits.  A fused consumer reduces them in split order.
 size_t qmm_partial_ws_bytes(int64_t M, int64_t N, int64_t K) {
     if (K % 128 != 0) return kCounterBytes;
-    return kCounterBytes + make_plan(M, N, K, kEpiPartial, true).partial_bytes;
+    return kCounterBytes + make_plan_p32(M, N, K, kEpiPartial).partial_bytes;
 }
 int qmm_packed_partial(const void *x, const void *packed, int64_t M, int64_t N, int64_t K, void *workspace,
                        size_t ws_bytes, int *splits, const float **partial, hipStream_t st) {
-    if (N % 16 != 0 || K % 128 != 0) return set_error("qmm packed: N must be a multiple of 16 and K of 128");
+    if (N % 32 != 0 || K % 128 != 0) return set_error("qmm packed: N must be a multiple of 32 and K of 128");
     if (((uintptr_t)x % 16) != 0 || ((uintptr_t)packed % 16) != 0) return set_error("qmm packed: misaligned operand");
     if (!workspace) return set_error("qmm packed partial: needs a workspace");
-    const Plan p = make_plan(M, N, K, kEpiPartial, true);
+    const Plan p = make_plan_p32(M, N, K, kEpiPartial);
     *splits = p.splits;
     *partial = (const float *)((const char *)workspace + kCounterBytes);
     return qmm_launch(x, (const uint32_t *)packed, nullptr, nullptr, nullptr, nullptr, M, N, K, VX_F16, 0, 0,
@@ -1001,7 +1255,7 @@ extern "C" int vx_qmm_4bit_ex(const void *x, const uint32_t *qweight, const void
 }
 
 extern "C" size_t vx_qmm_workspace_size(int64_t m, int64_t n, int64_t k) {
-    size_t a = qmm_workspace_bytes(m, n, k, VX_EPI_STORE);
-    size_t b = qmm_workspace_bytes(m, n, k, VX_EPI_SWIGLU);
+    size_t a = qmm_workspace_bytes(m, n, k, VX_EPI_STORE, false);
+    size_t b = qmm_workspace_bytes(m, n, k, VX_EPI_SWIGLU, false);
     return a > b ? a : b;
 }

@@ -82,7 +82,7 @@ def qmm_pack_4bit(qweight, scales, biases):
     """Packed copy of MLX int4 g64 weights (f16 scales/biases) for qmm_4bit_packed."""
     n, kp = qweight.shape
     k = kp * 8
-    _need(n % 16 == 0 and k % 128 == 0, f"qmm_pack_4bit: N={n} must be a multiple of 16 and K={k} of 128")
+    _need(n % 32 == 0 and k % 128 == 0, f"qmm_pack_4bit: N={n} must be a multiple of 32 and K={k} of 128")
     _need(tuple(scales.shape) == (n, k // 64) and tuple(biases.shape) == (n, k // 64),
           "qmm_pack_4bit: scales/biases must be [N, K/64]")
     _contig("qmm_pack_4bit", qweight=qweight, scales=scales, biases=biases)
