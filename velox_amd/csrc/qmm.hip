@@ -625,9 +625,15 @@ __device__ __forceinline__ void store_acc32(const QmmArgs &a, const floatx16 (&a
             const int col = col0 + nt * 32;
             if (a.splits > 1 || a.epi == kEpiPartial) {
                 if (col >= a.N) continue;
+                // rows m0 + 32t + hr + ro, ro = 8*(i/4) + i%4: one 64-bit base per
+                // tile, 32-bit row offsets
+                const int r0 = m0 + 32 * t + hr;
+                float *pb = a.partial + ((int64_t)sp * a.M + r0) * a.N + col;
+                const int rem = a.M - r0;
+#pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    const int row = m0 + 32 * t + 8 * (i >> 2) + hr + (i & 3);
-                    if (row < a.M) a.partial[((int64_t)sp * a.M + row) * a.N + col] = v[i];
+                    const int ro = 8 * (i >> 2) + (i & 3);
+                    if (ro < rem) pb[ro * a.N] = v[i];
                 }
             } else if (a.epi == VX_EPI_SWIGLU) {
 #pragma unroll
@@ -681,20 +687,23 @@ __global__ __launch_bounds__(256) void qmm_f16_p32_kernel(QmmArgs a) {
     const int wave = tid >> 6;
     const int col0 = cb * (kWaves * NT * 32) + wave * NT * 32 + (lane & 31);
 
-    // activation pieces: unit u = tid + 256 i is fragment (j, t) = divmod(u / 64, MT), lane u % 64;
-    // rows past M re-read row M-1 (finite values whose results are never stored)
+    // activation pieces: unit u = tid + 256 i is row u / 16, 16-byte chunk u % 16 of the
+    // step's 128 k, so one wave instruction reads four whole 256-byte row segments.  In
+    // LDS, chunk c of row r sits at r * 16 + (c ^ (r % 16)): sixteen consecutive lanes
+    // then hit sixteen distinct 16-byte bank groups both when a row is stored and when
+    // a fragment (32 rows, one chunk) is read.  Rows past M re-read row M-1 (finite
+    // values whose results are never stored).
     const uint16_t *xh = (const uint16_t *)a.x;
     int xoff[UPT];
 #pragma unroll
     for (int i = 0; i < UPT; i++) {
         const int u = tid + 256 * i;
-        const int ln = u & 63;
-        const int jt = u >> 6;
-        const int j = jt / MT;
-        const int t = jt - j * MT;
-        const int row = min(m0 + 32 * t + (ln & 31), a.M - 1);
-        xoff[i] = row * a.K + 16 * j + 8 * (ln >> 5);
+        const int row = min(m0 + (u >> 4), a.M - 1);
+        xoff[i] = row * a.K + 8 * (u & 15);
     }
+    const int xst = (tid >> 4) * 16 + ((tid & 15) ^ ((tid >> 4) & 15));  // + 256 i for piece i
+    const int xrd = (lane & 31) * 16;                                     // + 512 t + (2 j ^ xsw)
+    const int xsw = (lane >> 5) ^ (lane & 15);
     const uint8_t *wblk[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
@@ -731,7 +740,7 @@ __global__ __launch_bounds__(256) void qmm_f16_p32_kernel(QmmArgs a) {
     // register ring in scratch memory
     auto stage = [&](int buf, const uint4 (&xv)[UPT]) {
 #pragma unroll
-        for (int i = 0; i < UPT; i++) xs[buf][tid + 256 * i] = make_uint4(xv[i].x, xv[i].y, xv[i].z, xv[i].w);
+        for (int i = 0; i < UPT; i++) xs[buf][xst + 256 * i] = make_uint4(xv[i].x, xv[i].y, xv[i].z, xv[i].w);
     };
     auto step = [&](int st, auto slot_c) {
         constexpr int I = decltype(slot_c)::value;
@@ -756,7 +765,7 @@ __global__ __launch_bounds__(256) void qmm_f16_p32_kernel(QmmArgs a) {
         half8_t af[2][MT], bq[2][NT];
         auto lds_a = [&](int j, int c) {
 #pragma unroll
-            for (int t = 0; t < MT; t++) af[c][t] = __builtin_bit_cast(half8_t, xs[buf][(j * MT + t) * 64 + lane]);
+            for (int t = 0; t < MT; t++) af[c][t] = __builtin_bit_cast(half8_t, xs[buf][xrd + 512 * t + ((2 * j) ^ xsw)]);
         };
         auto deq_b = [&](int j, int c) {
 #pragma unroll
@@ -804,6 +813,393 @@ __global__ __launch_bounds__(256) void qmm_f16_p32_kernel(QmmArgs a) {
     if constexpr (R > 4) if (st + 3 < s_hi) step(st + 3, std::integral_constant<int, 3 % R>{});
     if constexpr (R > 5) if (st + 4 < s_hi) step(st + 4, std::integral_constant<int, 4 % R>{});
     store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16-byte LDS read at a byte address, issued outside the compiler's model of
+// LDS.  Activations reach LDS by DMA (global_load_lds), and the compiler
+// guards every LDS read it can see with a full vmcnt(0) after such a DMA,
+// which would drain the whole prefetch ring each step.  The caller orders the
+// read after its own vmcnt wait and barrier, and waits with lgkm_wait before
+// using the result.
+template <int OFF>
+__device__ __forceinline__ half8_t lds_read16(uint32_t addr) {
+    uint4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return __builtin_bit_cast(half8_t, v);
+}
+
+// s_waitcnt lgkmcnt(N), then an empty asm over the fragments so that their
+// uses cannot be scheduled above the wait.
+template <int N, int MT>
+__device__ __forceinline__ void lgkm_wait(half8_t (&f)[MT]) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
+#pragma unroll
+    for (int t = 0; t < MT; t++) asm volatile("" : "+v"(f[t]));
+}
+
+// One lane-strided DMA of 16 bytes per lane from global memory into LDS
+// (lane l lands at lds + 16 l), also outside the compiler's view: were the
+// compiler to see an LDS DMA among its pending loads, it would answer every
+// later wait with vmcnt(0).  vm_wait orders it.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N));
+}
+
+// The packed GEMM with the activations staged by LDS DMA.  Same tiles and
+// weight stream as qmm_f16_p32_kernel; the difference is where step s+P's
+// activations wait: in one of P+1 LDS buffers (global_load_lds_dwordx4, no
+// registers), so the prefetch depth no longer costs VGPRs and no VGPR->LDS
+// copy is issued.  Per step and wave: 2*MT DMA instructions, each filling
+// 1 KB = four 256-byte activation rows (row r, chunk c at r*16 + (c ^ r%16),
+// the bank-spread layout), then 3*NT weight loads into the register ring.
+// Step s begins with vmcnt((P-1) * (2*MT + 3*NT)): step s's DMA and weights
+// have landed while the P-1 later steps stay in flight; a barrier then makes
+// every wave's DMA visible and proves that the buffer refilled next was
+// read to the end by everyone.
+template <int MT, int NT, int P>
+__global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
+    constexpr int R = P + 1;
+    static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
+    constexpr int UX = 2 * MT;             // DMA instructions per wave per step
+    constexpr int UW = 3 * NT;             // weight loads per wave per step
+    constexpr int BUF = MT * 512;          // 16-byte slots per buffer (MT * 32 rows x 16 chunks)
+    constexpr int VM = (P - 1) * (UX + UW);
+    static_assert(VM < 64, "vmcnt range");
+    __shared__ __align__(256) uint4 xs[R * BUF];
+
+    const int bid = blockIdx.x;
+    const int item = (bid & 7) * a.per_xcd + (bid >> 3);
+    if (item >= a.total_items) return;
+    const int cb = item / a.splits;
+    const int sp = item - cb * a.splits;
+    const int m0 = blockIdx.y * MT * 32;
+    const int s_lo = sp * a.sps;
+    const int s_hi = min(a.S, s_lo + a.sps);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col0 = cb * (kWaves * NT * 32) + wave * NT * 32 + (lane & 31);
+
+    // DMA instruction g of wave w fills slots [64 (4g + w), +64): lane l takes
+    // row 16g + 4w + l/16 and chunk (l%16) ^ (row%16).  Rows past M re-read
+    // row M-1 (finite values whose results are never stored).
+    const uint16_t *xh = (const uint16_t *)a.x;
+    int xoff[UX];
+    {
+        const int rl = 4 * wave + (lane >> 4);
+        const int c = (lane & 15) ^ (rl & 15);
+#pragma unroll
+        for (int g = 0; g < UX; g++) xoff[g] = min(m0 + 16 * g + rl, a.M - 1) * a.K + 8 * c;
+    }
+    // fragment (j, t) of lane L: row 32t + L%32, chunk 2j + L/32, at byte
+    // 8192 t + 256 (L%32) + 16 ((2j + L/32) ^ L%16) = 8192 t + (xrd ^ 32j)
+    const uint32_t xs_addr = (uint32_t)(uintptr_t)(lds_void_t *)xs;
+    const uint32_t xs_wave = __builtin_amdgcn_readfirstlane(xs_addr + wave * 64 * 16);
+    const uint32_t xrd = xs_addr + (lane & 31) * 256 + 16 * ((lane >> 5) ^ (lane & 15));
+
+    const uint8_t *wblk[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tile = min(col0 / 32 + nt, a.N / 32 - 1);
+        wblk[nt] = (const uint8_t *)a.w + (int64_t)tile * a.S * kPackBlock;
+    }
+    constexpr uint32_t kLoHalf = 0x01000100u, kHiHalf = 0x03020302u;
+    const DqConst dq = dq_const();
+
+    floatx16 acc[MT][NT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[t][nt][i] = 0.f;
+
+    uint4 wlo[R][NT], whi[R][NT];
+    uint2 sr[R][NT];
+
+    auto issue = [&](int st, int buf, uint4 (&w0)[NT], uint4 (&w1)[NT], uint2 (&sv)[NT]) {
+#pragma unroll
+        for (int g = 0; g < UX; g++)
+            dma16(xh + xoff[g] + st * 128, xs_wave + (uint32_t)(buf * BUF + 256 * g) * 16);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const uint8_t *bp = wblk[nt] + (int64_t)st * kPackBlock;
+            w0[nt] = *(const uint4 *)(bp + lane * 16);
+            w1[nt] = *(const uint4 *)(bp + 1024 + lane * 16);
+            sv[nt] = *(const uint2 *)(bp + 2048 + (lane & 31) * 8);
+        }
+    };
+    auto step = [&](int st, auto slot_c) {
+        constexpr int I = decltype(slot_c)::value;
+        constexpr int NX = (I + P) % R;
+        vm_wait<VM>();
+        __builtin_amdgcn_s_barrier();
+        issue(min(st + P, s_hi - 1), NX, wlo[NX], whi[NX], sr[NX]);
+        __builtin_amdgcn_sched_barrier(0);
+        half2_t s2[NT][2], b2[NT][2];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            s2[nt][0] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].x, sr[I][nt].x, kLoHalf));
+            b2[nt][0] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].x, sr[I][nt].x, kHiHalf));
+            s2[nt][1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].y, sr[I][nt].y, kLoHalf));
+            b2[nt][1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sr[I][nt].y, sr[I][nt].y, kHiHalf));
+        }
+        const uint32_t base = xrd + I * MT * 8192;
+        half8_t af[2][MT], bq[2][NT];
+        auto lds_a = [&](int j, int c) {
+            const uint32_t ad = base ^ (32u * j);
+            if constexpr (MT > 0) af[c][0] = lds_read16<0>(ad);
+            if constexpr (MT > 1) af[c][1] = lds_read16<8192>(ad);
+            if constexpr (MT > 2) af[c][2] = lds_read16<16384>(ad);
+        };
+        auto deq_b = [&](int j, int c) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint4 q = (j >> 2) ? whi[I][nt] : wlo[I][nt];
+                const uint32_t word = (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
+                bq[c][nt] = dequant8(word, s2[nt][j >> 2], b2[nt][j >> 2], dq);
+            }
+        };
+        lds_a(0, 0);
+        deq_b(0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            // sub-step j+1's fragments are requested before sub-step j's MFMAs,
+            // whose own fragments are then waited for (MT reads stay in flight)
+            if (j < 7) {
+                lds_a(j + 1, (j + 1) & 1);
+                lgkm_wait<MT, MT>(af[j & 1]);
+            } else {
+                lgkm_wait<0, MT>(af[j & 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (j < 7) deq_b(j + 1, (j + 1) & 1);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][t], bq[j & 1][nt], acc[t][nt], 0, 0, 0);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < P; i++) issue(min(s_lo + i, s_hi - 1), i, wlo[i], whi[i], sr[i]);
+
+    int st = s_lo;
+    for (; st + R <= s_hi; st += R) {
+        step(st + 0, std::integral_constant<int, 0>{});
+        if constexpr (R > 1) step(st + 1, std::integral_constant<int, 1 % R>{});
+        if constexpr (R > 2) step(st + 2, std::integral_constant<int, 2 % R>{});
+        if constexpr (R > 3) step(st + 3, std::integral_constant<int, 3 % R>{});
+        if constexpr (R > 4) step(st + 4, std::integral_constant<int, 4 % R>{});
+        if constexpr (R > 5) step(st + 5, std::integral_constant<int, 5 % R>{});
+    }
+    // tail: fewer than R steps remain; slot of step st + i is i
+    if (st < s_hi) step(st, std::integral_constant<int, 0>{});
+    if constexpr (R > 2) if (st + 1 < s_hi) step(st + 1, std::integral_constant<int, 1 % R>{});
+    if constexpr (R > 3) if (st + 2 < s_hi) step(st + 2, std::integral_constant<int, 2 % R>{});
+    if constexpr (R > 4) if (st + 3 < s_hi) step(st + 3, std::integral_constant<int, 3 % R>{});
+    if constexpr (R > 5) if (st + 4 < s_hi) step(st + 4, std::integral_constant<int, 4 % R>{});
+    // the clamped prefetches past the last step still write LDS: drain them
+    // before the workgroup's LDS can be handed to another workgroup
+    vm_wait<0>();
+    store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
+}
+
+// The packed GEMM on eight waves: waves w and w+4 share the 32-column tiles
+// of slot w%4 and split each 128-wide k step, the first taking MFMAs 0..3
+// (packed words 0..3, the step's first scale group), the second MFMAs 4..7.
+// Two waves per SIMD then hide each other's LDS and dequant latency, a step
+// costs half the MFMA chain of the four-wave kernel, and each wave streams
+// half the weight bytes.  Activations arrive by LDS DMA as in
+// qmm_f16_dma_kernel (MT DMA instructions per wave per step); the two
+// halves' accumulators are summed through LDS once, at the end, by the
+// first wave of each pair.  No early exit: surplus workgroups of the last
+// XCD row recompute the last item and store nothing, so every kernel
+// argument is requested in one batch at entry.
+template <int MT, int NT, int P>
+__global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
+    constexpr int R = P + 1;
+    static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
+    constexpr int UX = MT;
+    constexpr int UW = 2 * NT;
+    constexpr int BUF = MT * 512;
+    constexpr int VM = (P - 1) * (UX + UW);
+    static_assert(VM < 64, "vmcnt range");
+    constexpr int XSLOTS = R * BUF;
+    constexpr int CSLOTS = 4 * MT * NT * 16 * 64 / 4;  // float4 slots of the pair combine
+    __shared__ __align__(256) uint4 xs[XSLOTS > CSLOTS ? XSLOTS : CSLOTS];
+
+    const int bid = blockIdx.x;
+    const int item0 = (bid & 7) * a.per_xcd + (bid >> 3);
+    const bool live = item0 < a.total_items;
+    const int item = live ? item0 : a.total_items - 1;
+    const int cb = item / a.splits;
+    const int sp = item - cb * a.splits;
+    const int m0 = blockIdx.y * MT * 32;
+    const int s_lo = sp * a.sps;
+    const int s_hi = min(a.S, s_lo + a.sps);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = wave >> 2;
+    const int wc = wave & 3;
+    const int col0 = cb * (kWaves * NT * 32) + wc * NT * 32 + (lane & 31);
+
+    // DMA instruction g of wave w fills slots [64 (8g + w), +64): lane l takes
+    // row 32g + 4w + l/16, chunk (l%16) ^ (row%16).  Rows past M re-read row M-1.
+    const uint16_t *xh = (const uint16_t *)a.x;
+    int xoff[UX];
+    {
+        const int rl = 4 * wave + (lane >> 4);
+        const int c = (lane & 15) ^ (rl & 15);
+#pragma unroll
+        for (int g = 0; g < UX; g++) xoff[g] = min(m0 + 32 * g + rl, a.M - 1) * a.K + 8 * c;
+    }
+    const uint32_t xs_addr = (uint32_t)(uintptr_t)(lds_void_t *)xs;
+    const uint32_t xs_wave = __builtin_amdgcn_readfirstlane(xs_addr + wave * 64 * 16);
+    // fragment (j, t), j = 4 kh + jj: byte 8192 t + (xrd ^ 32 j)
+    const uint32_t xrd = (xs_addr + (lane & 31) * 256 + 16 * ((lane >> 5) ^ (lane & 15))) ^ (128u * kh);
+
+    const uint8_t *wblk[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tile = min(col0 / 32 + nt, a.N / 32 - 1);
+        wblk[nt] = (const uint8_t *)a.w + (int64_t)tile * a.S * kPackBlock;
+    }
+    const int wq_off = kh * 1024 + lane * 16;
+    const int sb_off = 2048 + (lane & 31) * 8 + kh * 4;
+    constexpr uint32_t kLoHalf = 0x01000100u, kHiHalf = 0x03020302u;
+    const DqConst dq = dq_const();
+
+    floatx16 acc[MT][NT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[t][nt][i] = 0.f;
+
+    uint4 wq[R][NT];
+    uint32_t sb[R][NT];
+
+    auto issue = [&](int st, int buf, uint4 (&w)[NT], uint32_t (&sv)[NT]) {
+#pragma unroll
+        for (int g = 0; g < UX; g++) dma16(xh + xoff[g] + st * 128, xs_wave + (uint32_t)(buf * BUF + 512 * g) * 16);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const uint8_t *bp = wblk[nt] + (int64_t)st * kPackBlock;
+            w[nt] = *(const uint4 *)(bp + wq_off);
+            sv[nt] = *(const uint32_t *)(bp + sb_off);
+        }
+    };
+    auto step = [&](int st, auto slot_c) {
+        constexpr int I = decltype(slot_c)::value;
+        constexpr int NX = (I + P) % R;
+        vm_wait<VM>();
+        __builtin_amdgcn_s_barrier();
+        issue(min(st + P, s_hi - 1), NX, wq[NX], sb[NX]);
+        __builtin_amdgcn_sched_barrier(0);
+        half2_t s2[NT], b2[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            s2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sb[I][nt], sb[I][nt], kLoHalf));
+            b2[nt] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(sb[I][nt], sb[I][nt], kHiHalf));
+        }
+        const uint32_t base = xrd + I * MT * 8192;
+        half8_t af[2][MT], bq[2][NT];
+        auto lds_a = [&](int jj, int c) {
+            const uint32_t ad = base ^ (32u * jj);
+            if constexpr (MT > 0) af[c][0] = lds_read16<0>(ad);
+            if constexpr (MT > 1) af[c][1] = lds_read16<8192>(ad);
+            if constexpr (MT > 2) af[c][2] = lds_read16<16384>(ad);
+        };
+        auto deq_b = [&](int jj, int c) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint4 q = wq[I][nt];
+                const uint32_t word = jj == 0 ? q.x : jj == 1 ? q.y : jj == 2 ? q.z : q.w;
+                bq[c][nt] = dequant8(word, s2[nt], b2[nt], dq);
+            }
+        };
+        lds_a(0, 0);
+        deq_b(0, 0);
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            if (jj < 3) {
+                lds_a(jj + 1, (jj + 1) & 1);
+                lgkm_wait<MT, MT>(af[jj & 1]);
+            } else {
+                lgkm_wait<0, MT>(af[jj & 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (jj < 3) deq_b(jj + 1, (jj + 1) & 1);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[jj & 1][t], bq[jj & 1][nt], acc[t][nt], 0, 0, 0);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < P; i++) issue(min(s_lo + i, s_hi - 1), i, wq[i], sb[i]);
+
+    int st = s_lo;
+    for (; st + R <= s_hi; st += R) {
+        step(st + 0, std::integral_constant<int, 0>{});
+        if constexpr (R > 1) step(st + 1, std::integral_constant<int, 1 % R>{});
+        if constexpr (R > 2) step(st + 2, std::integral_constant<int, 2 % R>{});
+        if constexpr (R > 3) step(st + 3, std::integral_constant<int, 3 % R>{});
+        if constexpr (R > 4) step(st + 4, std::integral_constant<int, 4 % R>{});
+        if constexpr (R > 5) step(st + 5, std::integral_constant<int, 5 % R>{});
+    }
+    if (st < s_hi) step(st, std::integral_constant<int, 0>{});
+    if constexpr (R > 2) if (st + 1 < s_hi) step(st + 1, std::integral_constant<int, 1 % R>{});
+    if constexpr (R > 3) if (st + 2 < s_hi) step(st + 2, std::integral_constant<int, 2 % R>{});
+    if constexpr (R > 4) if (st + 3 < s_hi) step(st + 3, std::integral_constant<int, 3 % R>{});
+    if constexpr (R > 5) if (st + 4 < s_hi) step(st + 4, std::integral_constant<int, 4 % R>{});
+    vm_wait<0>();
+
+    // pair combine: the k-half-1 wave of slot wc hands its accumulators to the
+    // k-half-0 wave through LDS (float4 slot ((wc, t, nt) * 4 + q) * 64 + lane)
+    __syncthreads();
+    float4 *cs = (float4 *)xs;
+    if (kh == 1) {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    cs[(((wc * MT + t) * NT + nt) * 4 + q) * 64 + lane] =
+                        make_float4(acc[t][nt][4 * q], acc[t][nt][4 * q + 1], acc[t][nt][4 * q + 2], acc[t][nt][4 * q + 3]);
+    }
+    __syncthreads();
+    if (kh == 0 && live) {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 o = cs[(((wc * MT + t) * NT + nt) * 4 + q) * 64 + lane];
+                    acc[t][nt][4 * q] += o.x;
+                    acc[t][nt][4 * q + 1] += o.y;
+                    acc[t][nt][4 * q + 2] += o.z;
+                    acc[t][nt][4 * q + 3] += o.w;
+                }
+        store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
+    }
 }
 
 // Split-K finish: sum the partials of each output in split order, then the
@@ -873,6 +1269,7 @@ __global__ void add_bias_kernel(void *y, const void *bias, int64_t m, int64_t n)
 struct Plan {
     bool stream;  // f16 streaming kernel (else the LDS-chunked kernel)
     bool p32;     // packed weights on the 32x32 MFMA kernel
+    bool k2;      // ... on its eight-wave, k-split form
     int MT, NT, P, splits, gps, sps, col_blocks, m_blocks, per_xcd, total_items;
     size_t partial_bytes;
 };
@@ -901,11 +1298,12 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     int nt = env_int("VX_QMM_NT", 1);
     p.NT = nt;
     p.P = p32_depth(p.MT, nt);
+    p.k2 = env_int("VX_QMM_K2", 0) != 0;
     p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 32);
     const int items = p.col_blocks * p.m_blocks;
     // three row tiles hold one workgroup per CU (registers); fewer hold two.
     // Partial mode aims a little lower: its consumer reads every split.
-    const double per_cu = p.MT >= 3 ? 1.0 : 2.0;
+    const double per_cu = p.k2 ? env_int("VX_QMM_PERCU", 1) : (p.MT >= 3 ? 1.0 : 2.0);
     const double target = per_cu * cus * (epi == kEpiPartial ? 0.9 : 1.0);
     int splits = std::max(1, (int)(target / std::max(1, items) + 0.5));
     if (epi == kEpiPartial) splits = std::min(splits, kMaxPartialSplits);
@@ -1014,7 +1412,52 @@ void launch_p32(const QmmArgs &a, const Plan &p, hipStream_t st) {
     launch_reduce(a, p, st);
 }
 
+template <int MT, int NT, int P>
+void launch_dma(const QmmArgs &a, const Plan &p, hipStream_t st) {
+    dim3 grid(p.per_xcd * 8, p.m_blocks);
+    hipLaunchKernelGGL((qmm_f16_dma_kernel<MT, NT, P>), grid, dim3(256), 0, st, a);
+    launch_reduce(a, p, st);
+}
+
+template <int MT, int NT, int P>
+void launch_k2(const QmmArgs &a, const Plan &p, hipStream_t st) {
+    dim3 grid(p.per_xcd * 8, p.m_blocks);
+    hipLaunchKernelGGL((qmm_f16_k2_kernel<MT, NT, P>), grid, dim3(512), 0, st, a);
+    launch_reduce(a, p, st);
+}
+
 int dispatch_p32(const QmmArgs &a, const Plan &p, hipStream_t st) {
+    if (p.k2) {
+        const int P = env_int("VX_QMM_P", p.MT == 3 ? 2 : 3);
+#define VX_KCASE(mt, nt, pp)                             \
+        if (p.MT == mt && p.NT == nt && P == pp) {       \
+            launch_k2<mt, nt, pp>(a, p, st);             \
+            return 0;                                    \
+        }
+        VX_KCASE(1, 1, 2) VX_KCASE(1, 1, 3) VX_KCASE(1, 1, 4)
+        VX_KCASE(2, 1, 2) VX_KCASE(2, 1, 3)
+        VX_KCASE(3, 1, 2) VX_KCASE(3, 1, 3)
+        VX_KCASE(1, 2, 3) VX_KCASE(3, 2, 2)
+#undef VX_KCASE
+        return set_error("qmm: no eight-wave kernel for tile plan");
+    }
+    if (env_int("VX_QMM_DMA", 1)) {
+        const int P = env_int("VX_QMM_P", p.MT == 3 ? 2 : 3);
+#define VX_DCASE(mt, nt, pp)                             \
+        if (p.MT == mt && p.NT == nt && P == pp) {       \
+            launch_dma<mt, nt, pp>(a, p, st);            \
+            return 0;                                    \
+        }
+        VX_DCASE(1, 1, 2) VX_DCASE(1, 1, 3) VX_DCASE(1, 1, 4) VX_DCASE(1, 1, 5)
+        VX_DCASE(1, 2, 2) VX_DCASE(1, 2, 3) VX_DCASE(1, 2, 4)
+        VX_DCASE(2, 1, 2) VX_DCASE(2, 1, 3) VX_DCASE(2, 1, 4)
+        VX_DCASE(2, 2, 2) VX_DCASE(2, 2, 3)
+        VX_DCASE(3, 1, 2) VX_DCASE(3, 1, 3) VX_DCASE(3, 1, 4)
+        VX_DCASE(3, 2, 2) VX_DCASE(3, 2, 3)
+        VX_DCASE(3, 4, 1) VX_DCASE(3, 4, 2)
+#undef VX_DCASE
+        return set_error("qmm: no DMA kernel for tile plan");
+    }
 #define VX_CASE(mt, nt)                \
     if (p.MT == mt && p.NT == nt) {    \
         launch_p32<mt, nt>(a, p, st);  \
