@@ -1015,6 +1015,58 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
 }
 
+// Split-partial store of the eight-wave kernel (one 32-column tile per wave
+// pair).  Row-major tiles [slot][t][32 rows][kRowStride floats] in LDS: the
+// k-half-1 wave writes its accumulators (lane L, element i -> row
+// 8*(i/4) + 4*(L/32) + i%4, column L%32), the k-half-0 wave adds its own in
+// place, and then every thread stores 4 consecutive columns of a row per
+// 16-byte store (eight lanes per 128-byte row piece).  A row stride of 40
+// floats puts the two half-waves of each LDS access on disjoint banks.
+constexpr int kRowStride = 40;
+template <int MT>
+__device__ __forceinline__ void store_partial_rows(const QmmArgs &a, const floatx16 (&acc)[MT][1], float *lds,
+                                                   int m0, int colb, int sp, int kh, int wc, int lane, int tid,
+                                                   bool live) {
+    const int hr = 4 * (lane >> 5);
+    const int c = lane & 31;
+    float *tile0 = lds + wc * MT * 32 * kRowStride;
+    if (kh == 1) {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                tile0[(t * 32 + 8 * (i >> 2) + hr + (i & 3)) * kRowStride + c] = acc[t][0][i];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float *p = tile0 + (t * 32 + 8 * (i >> 2) + hr + (i & 3)) * kRowStride + c;
+                *p = *p + acc[t][0][i];
+            }
+    }
+    __syncthreads();
+    if (!live) return;
+    // piece e = tid + 512 k: slot e / (256 MT), tile (e / 256) % MT, row (e / 8) % 32, columns 4 (e % 8) ..
+    constexpr int PIECES = 4 * MT * 256;
+#pragma unroll
+    for (int k = 0; k < PIECES / 512; k++) {
+        const int e = tid + 512 * k;
+        const int slot = e / (256 * MT);
+        const int t = (e >> 8) % MT;
+        const int r = (e >> 3) & 31;
+        const int c4 = e & 7;
+        const int row = m0 + 32 * t + r;
+        const int col = colb + slot * 32 + 4 * c4;
+        if (row < a.M && col < a.N) {
+            const float4 v = *(const float4 *)(lds + ((slot * MT + t) * 32 + r) * kRowStride + 4 * c4);
+            *(float4 *)(a.partial + ((int64_t)sp * a.M + row) * a.N + col) = v;
+        }
+    }
+}
+
 // The packed GEMM on eight waves: waves w and w+4 share the 32-column tiles
 // of slot w%4 and split each 128-wide k step, the first taking MFMAs 0..3
 // (packed words 0..3, the step's first scale group), the second MFMAs 4..7.
@@ -1037,7 +1089,9 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     static_assert(VM < 64, "vmcnt range");
     constexpr int XSLOTS = R * BUF;
     constexpr int CSLOTS = 4 * MT * NT * 16 * 64 / 4;  // float4 slots of the pair combine
-    __shared__ __align__(256) uint4 xs[XSLOTS > CSLOTS ? XSLOTS : CSLOTS];
+    constexpr int RSLOTS = 4 * MT * 32 * kRowStride / 4;  // ... of the row-major partial tiles
+    constexpr int ESLOTS = CSLOTS > RSLOTS ? CSLOTS : RSLOTS;
+    __shared__ __align__(256) uint4 xs[XSLOTS > ESLOTS ? XSLOTS : ESLOTS];
 
     const int bid = blockIdx.x;
     const int item0 = (bid & 7) * a.per_xcd + (bid >> 3);
@@ -1170,6 +1224,16 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     if constexpr (R > 5) if (st + 4 < s_hi) step(st + 4, std::integral_constant<int, 4 % R>{});
     vm_wait<0>();
 
+    if constexpr (NT == 1) {
+        if (a.splits > 1 || a.epi == kEpiPartial) {
+            // split partials: the pair's sum is formed in LDS in row-major
+            // tiles, then all eight waves store 16-byte row pieces
+            __syncthreads();
+            store_partial_rows<MT>(a, acc, (float *)xs, m0, cb * (kWaves * 32), sp, kh, wc, lane, tid, live);
+            return;
+        }
+    }
+
     // pair combine: the k-half-1 wave of slot wc hands its accumulators to the
     // k-half-0 wave through LDS (float4 slot ((wc, t, nt) * 4 + q) * 64 + lane)
     __syncthreads();
@@ -1298,7 +1362,11 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     int nt = env_int("VX_QMM_NT", 1);
     p.NT = nt;
     p.P = p32_depth(p.MT, nt);
-    p.k2 = env_int("VX_QMM_K2", 0) != 0;
+    // the eight-wave kernel for one row tile (draft rows) below LM-head
+    // widths; for three row tiles it is chosen below when the K range per
+    // workgroup is short
+    const int k2_env = env_int("VX_QMM_K2", -1);
+    p.k2 = k2_env >= 0 ? k2_env != 0 : (p.MT == 1 && N <= 65536 && nt == 1);
     p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 32);
     const int items = p.col_blocks * p.m_blocks;
     // three row tiles hold one workgroup per CU (registers); fewer hold two.
@@ -1318,6 +1386,7 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     p.splits = splits;
     p.sps = sps;
     p.gps = 2 * sps;
+    if (k2_env < 0 && p.MT == 3 && nt == 1 && sps <= 4) p.k2 = true;
     p.total_items = p.col_blocks * p.splits;
     p.per_xcd = (int)vx_cdiv(p.total_items, 8);
     p.partial_bytes = (p.splits > 1 || epi == kEpiPartial) ? (size_t)p.splits * M * N * 4 : 0;
