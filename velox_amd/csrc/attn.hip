@@ -90,7 +90,7 @@ __device__ __forceinline__ void row_info(const AttnArgs &a, int seq, int &r_seq,
 template <int KT, int D, int QT>
 constexpr size_t attn_lds_bytes() {
     constexpr size_t vt = (size_t)kAttnWaves * D * (kKeyBlock + 4) * 2;
-    constexpr size_t comb = (size_t)(kAttnWaves - 1) * ((D / 16) * QT * 4 + 2 * QT) * 64 * 4;
+    constexpr size_t comb = (size_t)kAttnWaves * ((D / 16) * QT * 4 + 2 * QT) * 64 * 4;
     return vt > comb ? vt : comb;
 }
 
@@ -173,25 +173,28 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     for (int kb = k_lo + wave * kKeyBlock; kb < k_hi; kb += kAttnWaves * kKeyBlock) {
         // ---- request K (4 tiles of 16 keys, lane = key within a tile) and V
         // (lane = key) of the block together, so both round trips overlap
+        // lane l looks up the page of key kb + l once; the K rows take theirs
+        // by lane exchange, so one block-table round trip precedes both
+        const int vkey = kb + lane;
+        const int vpage = min((int)btr[min(vkey / a.ps, a.max_blocks - 1)], a.num_pages - 1);
         frag kf[4][DK];
 #pragma unroll
         for (int mt = 0; mt < 4; mt++) {
             const int key = kb + mt * 16 + lq;
-            const int blk = min(key / a.ps, a.max_blocks - 1);
-            const int page = min((int)btr[blk], a.num_pages - 1);
+            const int page = __shfl(vpage, mt * 16 + lq);
             const uint16_t *kr = (const uint16_t *)a.k + page * page_stride + hk * head_stride + (int64_t)(key % a.ps) * D;
 #pragma unroll
             for (int ks = 0; ks < DK; ks++) kf[mt][ks] = __builtin_bit_cast(frag, *(const uint4 *)(kr + ks * 32 + lg * 8));
         }
         uint4 vraw[D / 8];
         {
-            const int key = kb + lane;
-            const int blk = min(key / a.ps, a.max_blocks - 1);
-            const int page = min((int)btr[blk], a.num_pages - 1);
-            const uint16_t *vr = (const uint16_t *)a.v + page * page_stride + hk * head_stride + (int64_t)(key % a.ps) * D;
+            const uint16_t *vr = (const uint16_t *)a.v + vpage * page_stride + hk * head_stride + (int64_t)(vkey % a.ps) * D;
 #pragma unroll
             for (int c = 0; c < D / 8; c++) vraw[c] = *(const uint4 *)(vr + c * 8);
         }
+        // keep the V requests ahead of the K . Q^T products: the compiler
+        // would otherwise issue them after waiting for K
+        __builtin_amdgcn_sched_barrier(0);
         // ---- S^T = K . Q^T
         floatx4 s[4][QT];
 #pragma unroll
@@ -291,11 +294,14 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
         }
     }
 
-    // ---- merge the four waves' partials (key order = wave order) into wave 0
+    // ---- merge the four waves' partials: every wave publishes (m, l, O) and
+    // then finishes the d tiles [TPW*w, TPW*(w+1)) for all of its queries,
+    // summing the waves in wave order (deterministic)
+    constexpr int TPW = DT >= kAttnWaves ? DT / kAttnWaves : 1;
     __syncthreads();  // every wave is done with its V^T tile
     float *comb = (float *)smem;
-    if (wave > 0) {
-        float *dst = comb + (size_t)(wave - 1) * CSLOTS * 64 + lane;
+    {
+        float *dst = comb + (size_t)wave * CSLOTS * 64 + lane;
         int slot = 0;
 #pragma unroll
         for (int qt = 0; qt < QT; qt++) {
@@ -308,26 +314,36 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-    if (wave > 0) return;
+    const int i_lo = wave * TPW;
+    if (i_lo >= DT) return;
+    floatx4 om[TPW][QT];
+    float mm[QT], lm[QT];
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; w++) {
-        const float *src = comb + (size_t)(w - 1) * CSLOTS * 64 + lane;
-        int slot = 0;
+    for (int qt = 0; qt < QT; qt++) {
+        const int base = qt * (2 + DT * 4);
+        float mw[kAttnWaves], fw[kAttnWaves];
+        float M = -__builtin_inff();
 #pragma unroll
-        for (int qt = 0; qt < QT; qt++) {
-            const float mw = src[(slot++) * 64];
-            const float lw = src[(slot++) * 64];
-            const float m_new = fmaxf(m_run[qt], mw);
-            const bool dead = m_new == -__builtin_inff();
-            const float fa = dead ? 1.f : exp2f(m_run[qt] - m_new);
-            const float fb = dead ? 0.f : exp2f(mw - m_new);
-            l_run[qt] = l_run[qt] * fa + lw * fb;
-            m_run[qt] = m_new;
-#pragma unroll
-            for (int i = 0; i < DT; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) o[i][qt][r] = o[i][qt][r] * fa + src[(slot++) * 64] * fb;
+        for (int w = 0; w < kAttnWaves; w++) {
+            mw[w] = comb[((size_t)w * CSLOTS + base) * 64 + lane];
+            M = fmaxf(M, mw[w]);
         }
+        const bool dead = M == -__builtin_inff();
+        float L = 0.f;
+#pragma unroll
+        for (int t = 0; t < TPW; t++) om[t][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; w++) {
+            fw[w] = dead ? 0.f : exp2f(mw[w] - M);
+            L += comb[((size_t)w * CSLOTS + base + 1) * 64 + lane] * fw[w];
+#pragma unroll
+            for (int t = 0; t < TPW; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    om[t][qt][r] += comb[((size_t)w * CSLOTS + base + 2 + (i_lo + t) * 4 + r) * 64 + lane] * fw[w];
+        }
+        mm[qt] = M;
+        lm[qt] = L;
     }
 
     // ---- single split: write the output; else publish (m, l, O) for the merge
@@ -338,14 +354,14 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int qt = 0; qt < QT; qt++) {
             const int n = qt * 16 + lq;
-            if (lg == 0) {
-                pbase[n] = m_run[qt];
-                pbase[64 + n] = l_run[qt];
+            if (lg == 0 && wave == 0) {
+                pbase[n] = mm[qt];
+                pbase[64 + n] = lm[qt];
             }
 #pragma unroll
-            for (int i = 0; i < DT; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) pbase[128 + (int64_t)n * D + i * 16 + lg * 4 + r] = o[i][qt][r];
+            for (int t = 0; t < TPW; t++)
+                *(float4 *)(pbase + 128 + (int64_t)n * D + (i_lo + t) * 16 + lg * 4) =
+                    make_float4(om[t][qt][0], om[t][qt][1], om[t][qt][2], om[t][qt][3]);
         }
         return;
     }
@@ -354,17 +370,20 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
         if (q_row[qt] < 0) continue;
         const int n = qt * 16 + lq;
         const int hq = hk * a.G + (n % a.G);
-        const float inv = 1.0f / l_run[qt];
+        const float inv = 1.0f / lm[qt];
 #pragma unroll
-        for (int i = 0; i < DT; i++)
+        for (int t = 0; t < TPW; t++) {
+            uint16_t h[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int d = i * 16 + lg * 4 + r;
-                const int64_t oi = ((int64_t)q_row[qt] * a.h_q + hq) * D + d;
-                float val = o[i][qt][r] * inv;
+                float val = om[t][qt][r] * inv;
                 if (a.out_bf16_round) val = round_to<VX_BF16>(val);
-                ((uint16_t *)a.out)[oi] = MfmaT<KT>::cvt(val);
+                h[r] = MfmaT<KT>::cvt(val);
             }
+            const int64_t oi = ((int64_t)q_row[qt] * a.h_q + hq) * D + (i_lo + t) * 16 + lg * 4;
+            *(uint2 *)((uint16_t *)a.out + oi) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                                            (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+        }
     }
 }
 
