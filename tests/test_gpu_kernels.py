@@ -311,6 +311,22 @@ def test_verify_attention_chain_shuffled_pages(cuda, ctx):
     assert_allclose_elementwise("verify chain", got, ref, 1e-2, 1e-2)
 
 
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_verify_attention_head_dims(cuda, d, dt):
+    """Every head dim of the MFMA path (each stages V row-major with its own
+    chunk permutation and reads it back transposed), shuffled pages, two key
+    blocks per wave and a ragged last block."""
+    rng = np.random.default_rng(d)
+    B, R, ps, ctx = 3, 5, 16, 520
+    nb = (ctx + R + ps - 1) // ps
+    P = B * nb + 2
+    perm = rng.permutation(P)[: B * nb].reshape(B, nb)
+    got, ref = _prefill_case([R] * B, [ctx - 7, ctx - 90, ctx], perm, P, 17 + d, dt=dt, hq=8, hk=2, d=d)
+    tol = 1e-2 if dt == "f16" else 3e-2
+    assert_allclose_elementwise(f"verify d={d} {dt}", got, ref, tol, tol)
+
+
 def tree_4_2_2():
     """16 draft nodes (4 + 8 + 4) under the root: node 0 = root, depth-1 nodes
     1-4, each with 2 children (5-12), and nodes 5 and 6 each with 2 children

@@ -223,24 +223,33 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int qt = 0; qt < QT; qt++) {
             bmax[qt] = -__builtin_inff();
+            // visible keys: [lo, hi) for the causal rule (plus the window); the
+            // tree rule also tests the row's ancestor bits past the context
+            const int hi = q_row[qt] < 0 ? 0 : min(k_hi, a.tmask ? kv_end : q_lim[qt]);
+            const int lo = (win > 0 && q_lim[qt] > win) ? q_lim[qt] - win : 0;
+            if (a.tmask) {
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++)
+                for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = kb + mt * 16 + lg * 4 + r;
-                    bool vis = q_row[qt] >= 0 && key < k_hi;
-                    if (vis) {
-                        if (a.tmask) {
-                            if (key >= off) vis = (key - off) < 64 && ((q_mask[qt] >> (key - off)) & 1ull);
-                        } else {
-                            vis = key < q_lim[qt];
-                        }
-                        if (win > 0 && q_lim[qt] > win && key < q_lim[qt] - win) vis = false;
+                    for (int r = 0; r < 4; r++) {
+                        const int key = kb + mt * 16 + lg * 4 + r;
+                        bool vis = key >= lo && key < hi;
+                        if (key >= off) vis = vis && (key - off) < 64 && ((q_mask[qt] >> (key - off)) & 1ull);
+                        const float v = vis ? s[mt][qt][r] * a.scale_log2 : -__builtin_inff();
+                        s[mt][qt][r] = v;
+                        bmax[qt] = fmaxf(bmax[qt], v);
                     }
-                    const float v = vis ? s[mt][qt][r] * a.scale_log2 : -__builtin_inff();
-                    s[mt][qt][r] = v;
-                    bmax[qt] = fmaxf(bmax[qt], v);
-                }
+            } else {
+#pragma unroll
+                for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int key = kb + mt * 16 + lg * 4 + r;
+                        const float v = (key >= lo && key < hi) ? s[mt][qt][r] * a.scale_log2 : -__builtin_inff();
+                        s[mt][qt][r] = v;
+                        bmax[qt] = fmaxf(bmax[qt], v);
+                    }
+            }
             bmax[qt] = fmaxf(bmax[qt], __shfl_xor(bmax[qt], 16));
             bmax[qt] = fmaxf(bmax[qt], __shfl_xor(bmax[qt], 32));
         }
@@ -250,14 +259,14 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
         for (int qt = 0; qt < QT; qt++) {
             const float m_new = fmaxf(m_run[qt], bmax[qt]);
             const bool dead = m_new == -__builtin_inff();
-            const float alpha = dead ? 1.f : exp2f(m_run[qt] - m_new);
+            const float alpha = dead ? 1.f : __builtin_amdgcn_exp2f(m_run[qt] - m_new);
             float psum = 0.f;
             uint16_t ph[4][4];
 #pragma unroll
             for (int mt = 0; mt < 4; mt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float p = dead ? 0.f : exp2f(s[mt][qt][r] - m_new);
+                    const float p = dead ? 0.f : __builtin_amdgcn_exp2f(s[mt][qt][r] - m_new);
                     psum += p;
                     ph[mt][r] = MfmaT<KT>::cvt(p);
                 }
