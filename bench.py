@@ -181,8 +181,8 @@ def run_spec(args):
             "ms": agg["verify_ms"], "algorithmic_bytes": verify_bytes, "hbm_gbs": verify_gbs,
             "draft_ms": agg["draft_ms"], "accept_ms": agg["accept_ms"]},
         "roofline": {"bound": "hbm",
-                     "kernel": "qmm_f16_stream_kernel: the verify step's int4 GEMMs (36 layers x qkv, o, gate|up "
-                               "with its SwiGLU finish, down; plus the LM head), average per op",
+                     "kernel": "qmm_f16_dma_kernel / qmm_f16_k2_kernel: the verify step's int4 GEMMs (36 layers "
+                               "x qkv, o, gate|up with its SwiGLU finish, down; plus the LM head), average per op",
                      "achieved": qmm_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": None if qmm_gbs is None else qmm_gbs / PEAK_HBM_GBS,
                      "traffic": traffic_per_op(),

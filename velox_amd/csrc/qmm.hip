@@ -1375,6 +1375,12 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     const double target = per_cu * cus * (epi == kEpiPartial ? 0.9 : 1.0);
     int splits = std::max(1, (int)(target / std::max(1, items) + 0.5));
     if (epi == kEpiPartial) splits = std::min(splits, kMaxPartialSplits);
+    // SwiGLU on one row tile over at least half the CUs' worth of column
+    // blocks: one split on the eight-wave kernel, so the epilogue runs in
+    // place and no finishing kernel is launched (with three row tiles the
+    // in-place epilogue costs more than the finishing kernel)
+    const bool swiglu_whole = epi == VX_EPI_SWIGLU && nt == 1 && p.MT == 1 && 2 * items >= cus;
+    if (swiglu_whole) splits = 1;
     splits = env_int("VX_QMM_SPLITS", splits);
     splits = std::max(1, std::min(splits, S));
     int sps = (int)vx_cdiv(S, splits);
@@ -1386,7 +1392,7 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     p.splits = splits;
     p.sps = sps;
     p.gps = 2 * sps;
-    if (k2_env < 0 && p.MT == 3 && nt == 1 && sps <= 4) p.k2 = true;
+    if (k2_env < 0 && p.MT == 3 && nt == 1 && (sps <= 4 || swiglu_whole)) p.k2 = true;
     p.total_items = p.col_blocks * p.splits;
     p.per_xcd = (int)vx_cdiv(p.total_items, 8);
     p.partial_bytes = (p.splits > 1 || epi == kEpiPartial) ? (size_t)p.splits * M * N * 4 : 0;

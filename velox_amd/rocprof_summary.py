@@ -3,10 +3,11 @@
     python -m velox_amd.rocprof_summary trace RESULTS.db [--top N]
         per (kernel, grid) dispatch count and duration statistics
     python -m velox_amd.rocprof_summary verify RESULTS.db [--rounds R] [--pmc FILE.db ...]
-        the verify int4 GEMMs of the spec bench's timed rounds: every
-        qmm_f16_stream_kernel dispatch with an 80-row tile (<5, ...>) and a
-        one-row grid (prefill uses many row blocks), plus the SwiGLU finish
-        (qmm_reduce_kernel) that follows a gate|up dispatch; per-round sums
+        the verify int4 GEMMs of the spec bench's timed rounds: every packed
+        GEMM dispatch (qmm_f16_dma_kernel / qmm_f16_k2_kernel) with three
+        32-row tiles (<3, ...>, the 80 verify rows) and a one-row grid (prefill
+        uses many row blocks), plus the SwiGLU finish (qmm_reduce_kernel) that
+        follows a gate|up dispatch; per-round sums
         and the average per GEMM op, and with --pmc the FETCH_SIZE / WRITE_SIZE
         sums of the same dispatches scaled by the calibration copy
     python -m velox_amd.rocprof_summary calib RESULTS.db --bytes B
@@ -29,10 +30,12 @@ def _short(name: str) -> str:
 
 
 def dispatches(db: str):
-    """[(short name, start, end, grid_x, grid_y, dispatch_id)] in start order."""
+    """[(short name, start, end, workgroups along x, grid_y, dispatch_id)] in start order
+    (rocprofv3 records grid_x in work-items)."""
     c = sqlite3.connect(db)
-    rows = c.execute("select name, start, end, grid_x, grid_y, dispatch_id from kernels order by start").fetchall()
-    return [(_short(n), s, e, gx, gy, d) for n, s, e, gx, gy, d in rows]
+    rows = c.execute("select name, start, end, grid_x, grid_y, dispatch_id, workgroup_x from kernels "
+                     "order by start").fetchall()
+    return [(_short(n), s, e, gx // max(1, wx), gy, d) for n, s, e, gx, gy, d, wx in rows]
 
 
 def counters(db: str):
@@ -56,7 +59,7 @@ def cmd_trace(args):
     print(f"{'kernel':64s} {'grid (wg x, y)':>14s} {'n':>6s} {'total us':>10s} {'avg us':>8s} {'med us':>8s} {'min us':>8s}")
     for (n, gx, gy), v in sorted(st.items(), key=lambda kv: -sum(kv[1]))[: args.top]:
         v.sort()
-        print(f"{n[:64]:64s} {f'{gx // 256}x{gy}':>14s} {len(v):6d} {sum(v) / 1e3:10.1f} {sum(v) / len(v) / 1e3:8.2f} "
+        print(f"{n[:64]:64s} {f'{gx}x{gy}':>14s} {len(v):6d} {sum(v) / 1e3:10.1f} {sum(v) / len(v) / 1e3:8.2f} "
               f"{v[len(v) // 2] / 1e3:8.2f} {v[0] / 1e3:8.2f}")
 
 
@@ -65,8 +68,8 @@ def _verify_ops(ds, rounds):
     ops = []
     prev_gate_up = False
     for n, s, e, gx, gy, d in ds:
-        m = re.match(r"qmm_f16_stream_kernel<(\d+), (\d+), (\d+), (true|false)>", n)
-        if m and m.group(1) == "5" and gy == 1:
+        m = re.match(r"qmm_f16_(?:dma|k2)_kernel<(\d+), (\d+), (\d+)>", n)
+        if m and m.group(1) == "3" and gy == 1:
             ops.append([(n, s, e, d)])
             prev_gate_up = True
             continue
