@@ -815,6 +815,120 @@ __global__ __launch_bounds__(256) void qmm_f16_p32_kernel(QmmArgs a) {
     store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
 }
 
+// Row-major epilogue of the packed kernels (one 32-column tile per wave
+// slot).  The accumulators go to LDS as row-major tiles [slot][t][32 rows]
+// [kRowStride floats] (lane L, element i -> row 8*(i/4) + 4*(L/32) + i%4,
+// column L%32); a row stride of 40 floats puts the two half-waves of each
+// LDS access on disjoint banks.  Then every thread finishes four consecutive
+// columns of a row per step (eight lanes per 128-byte row piece): split
+// partials as one 16-byte store, STORE / RESIDUAL / SwiGLU with 8- or
+// 16-byte accesses, instead of sixteen scattered element stores per tile.
+constexpr int kRowStride = 40;
+
+template <int MT>
+__device__ __forceinline__ void acc_to_rows(const floatx16 (&acc)[MT][1], float *tile0, int lane, bool add) {
+    const int hr = 4 * (lane >> 5);
+    const int c = lane & 31;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float *p = tile0 + (t * 32 + 8 * (i >> 2) + hr + (i & 3)) * kRowStride + c;
+            *p = add ? *p + acc[t][0][i] : acc[t][0][i];
+        }
+}
+
+__device__ __forceinline__ void store4_dt(void *y, int64_t i, const float (&v)[4], int dt) {
+    if (dt == VX_F32) {
+        *(float4 *)((float *)y + i) = make_float4(v[0], v[1], v[2], v[3]);
+        return;
+    }
+    uint16_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) h[e] = dt == VX_F16 ? f32_to_f16_bits(v[e]) : f32_to_bf16_bits(v[e]);
+    *(uint2 *)((uint16_t *)y + i) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+}
+
+__device__ __forceinline__ void load4_dt(const void *p, int64_t i, float (&v)[4], int dt) {
+    if (dt == VX_F32) {
+        const float4 f = *(const float4 *)((const float *)p + i);
+        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+        return;
+    }
+    const uint2 w = *(const uint2 *)((const uint16_t *)p + i);
+    const uint16_t h[4] = {(uint16_t)(w.x & 0xffffu), (uint16_t)(w.x >> 16), (uint16_t)(w.y & 0xffffu),
+                           (uint16_t)(w.y >> 16)};
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = dt == VX_F16 ? f16_bits_to_f32(h[e]) : bf16_bits_to_f32(h[e]);
+}
+
+// Finish the row-major tiles of one workgroup (THREADS threads): columns
+// colb + 32*slot + 4*c4 .. +3 of rows m0 + 32t + r.
+template <int MT, int THREADS>
+__device__ __forceinline__ void finish_rows(const QmmArgs &a, const float *lds, int m0, int colb, int sp, int tid,
+                                            bool live) {
+    if (!live) return;
+    const bool partial = a.splits > 1 || a.epi == kEpiPartial;
+    if (a.epi == VX_EPI_SWIGLU && !partial) {
+        // per (slot, t, r): features 16*tile + 4*c4 .. +3, gate at columns
+        // 4*c4 .. and up at 16 + 4*c4 .. of the tile
+        constexpr int PIECES = 4 * MT * 32 * 4;
+#pragma unroll
+        for (int k = 0; k < (PIECES + THREADS - 1) / THREADS; k++) {
+            const int e = tid + THREADS * k;
+            if (PIECES % THREADS != 0 && e >= PIECES) break;
+            const int slot = e / (128 * MT);
+            const int t = (e >> 7) % MT;
+            const int r = (e >> 2) & 31;
+            const int c4 = e & 3;
+            const int row = m0 + 32 * t + r;
+            const int tile = colb / 32 + slot;
+            if (row >= a.M || tile * 32 >= a.N) continue;
+            const float *src = lds + ((slot * MT + t) * 32 + r) * kRowStride + 4 * c4;
+            const float4 g4 = *(const float4 *)src, u4 = *(const float4 *)(src + 16);
+            const float gv[4] = {g4.x, g4.y, g4.z, g4.w}, uv[4] = {u4.x, u4.y, u4.z, u4.w};
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float g = round_dt(gv[q] * a.acc_scale, a.round_dt);
+                const float u = round_dt(uv[q] * a.acc_scale, a.round_dt);
+                v[q] = round_dt(round_dt(silu_f(g), a.round_dt) * u, a.round_dt) * a.store_scale;
+            }
+            store4_dt(a.y, (int64_t)row * (a.N / 2) + tile * 16 + 4 * c4, v, a.y_dt);
+        }
+        return;
+    }
+    constexpr int PIECES = 4 * MT * 32 * 8;
+#pragma unroll
+    for (int k = 0; k < (PIECES + THREADS - 1) / THREADS; k++) {
+        const int e = tid + THREADS * k;
+        if (PIECES % THREADS != 0 && e >= PIECES) break;
+        const int slot = e / (256 * MT);
+        const int t = (e >> 8) % MT;
+        const int r = (e >> 3) & 31;
+        const int c4 = e & 7;
+        const int row = m0 + 32 * t + r;
+        const int col = colb + slot * 32 + 4 * c4;
+        if (row >= a.M || col >= a.N) continue;
+        const float4 s4 = *(const float4 *)(lds + ((slot * MT + t) * 32 + r) * kRowStride + 4 * c4);
+        if (partial) {
+            *(float4 *)(a.partial + ((int64_t)sp * a.M + row) * a.N + col) = s4;
+            continue;
+        }
+        const int64_t idx = (int64_t)row * a.N + col;
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+        float v[4], rv[4];
+        if (a.epi == VX_EPI_RESIDUAL) load4_dt(a.resid, idx, rv, a.y_dt);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            v[q] = round_dt(sv[q] * a.acc_scale, a.round_dt);
+            if (a.epi == VX_EPI_RESIDUAL) v[q] = round_dt(rv[q] + v[q], a.round_dt);
+            v[q] *= a.store_scale;
+        }
+        store4_dt(a.y, idx, v, a.y_dt);
+    }
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // 16-byte LDS read at a byte address, issued outside the compiler's model of
@@ -1012,58 +1126,13 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     // the clamped prefetches past the last step still write LDS: drain them
     // before the workgroup's LDS can be handed to another workgroup
     vm_wait<0>();
-    store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
-}
-
-// Split-partial store of the eight-wave kernel (one 32-column tile per wave
-// pair).  Row-major tiles [slot][t][32 rows][kRowStride floats] in LDS: the
-// k-half-1 wave writes its accumulators (lane L, element i -> row
-// 8*(i/4) + 4*(L/32) + i%4, column L%32), the k-half-0 wave adds its own in
-// place, and then every thread stores 4 consecutive columns of a row per
-// 16-byte store (eight lanes per 128-byte row piece).  A row stride of 40
-// floats puts the two half-waves of each LDS access on disjoint banks.
-constexpr int kRowStride = 40;
-template <int MT>
-__device__ __forceinline__ void store_partial_rows(const QmmArgs &a, const floatx16 (&acc)[MT][1], float *lds,
-                                                   int m0, int colb, int sp, int kh, int wc, int lane, int tid,
-                                                   bool live) {
-    const int hr = 4 * (lane >> 5);
-    const int c = lane & 31;
-    float *tile0 = lds + wc * MT * 32 * kRowStride;
-    if (kh == 1) {
-#pragma unroll
-        for (int t = 0; t < MT; t++)
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                tile0[(t * 32 + 8 * (i >> 2) + hr + (i & 3)) * kRowStride + c] = acc[t][0][i];
-    }
-    __syncthreads();
-    if (kh == 0) {
-#pragma unroll
-        for (int t = 0; t < MT; t++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float *p = tile0 + (t * 32 + 8 * (i >> 2) + hr + (i & 3)) * kRowStride + c;
-                *p = *p + acc[t][0][i];
-            }
-    }
-    __syncthreads();
-    if (!live) return;
-    // piece e = tid + 512 k: slot e / (256 MT), tile (e / 256) % MT, row (e / 8) % 32, columns 4 (e % 8) ..
-    constexpr int PIECES = 4 * MT * 256;
-#pragma unroll
-    for (int k = 0; k < PIECES / 512; k++) {
-        const int e = tid + 512 * k;
-        const int slot = e / (256 * MT);
-        const int t = (e >> 8) % MT;
-        const int r = (e >> 3) & 31;
-        const int c4 = e & 7;
-        const int row = m0 + 32 * t + r;
-        const int col = colb + slot * 32 + 4 * c4;
-        if (row < a.M && col < a.N) {
-            const float4 v = *(const float4 *)(lds + ((slot * MT + t) * 32 + r) * kRowStride + 4 * c4);
-            *(float4 *)(a.partial + ((int64_t)sp * a.M + row) * a.N + col) = v;
-        }
+    if constexpr (NT == 1 && R * BUF * 16 >= 4 * MT * 32 * kRowStride * 4) {
+        __syncthreads();
+        acc_to_rows<MT>(acc, (float *)xs + wave * MT * 32 * kRowStride, lane, false);
+        __syncthreads();
+        finish_rows<MT, 256>(a, (const float *)xs, m0, cb * (kWaves * 32), sp, tid, true);
+    } else {
+        store_acc32<MT, NT>(a, acc, m0, col0, sp, lane);
     }
 }
 
@@ -1225,13 +1294,16 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     vm_wait<0>();
 
     if constexpr (NT == 1) {
-        if (a.splits > 1 || a.epi == kEpiPartial) {
-            // split partials: the pair's sum is formed in LDS in row-major
-            // tiles, then all eight waves store 16-byte row pieces
-            __syncthreads();
-            store_partial_rows<MT>(a, acc, (float *)xs, m0, cb * (kWaves * 32), sp, kh, wc, lane, tid, live);
-            return;
-        }
+        // the pair's sum is formed in LDS as row-major tiles, then all eight
+        // waves finish four columns at a time
+        float *tile0 = (float *)xs + wc * MT * 32 * kRowStride;
+        __syncthreads();
+        if (kh == 1) acc_to_rows<MT>(acc, tile0, lane, false);
+        __syncthreads();
+        if (kh == 0) acc_to_rows<MT>(acc, tile0, lane, true);
+        __syncthreads();
+        finish_rows<MT, 512>(a, (const float *)xs, m0, cb * (kWaves * 32), sp, tid, live);
+        return;
     }
 
     // pair combine: the k-half-1 wave of slot wc hands its accumulators to the
@@ -1375,11 +1447,11 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     const double target = per_cu * cus * (epi == kEpiPartial ? 0.9 : 1.0);
     int splits = std::max(1, (int)(target / std::max(1, items) + 0.5));
     if (epi == kEpiPartial) splits = std::min(splits, kMaxPartialSplits);
-    // SwiGLU on one row tile over at least half the CUs' worth of column
-    // blocks: one split on the eight-wave kernel, so the epilogue runs in
-    // place and no finishing kernel is launched (with three row tiles the
-    // in-place epilogue costs more than the finishing kernel)
-    const bool swiglu_whole = epi == VX_EPI_SWIGLU && nt == 1 && p.MT == 1 && 2 * items >= cus;
+    // SwiGLU over at least half the CUs' worth of column blocks: one split on
+    // the eight-wave kernel, so the epilogue runs in place (row-major LDS
+    // epilogue) and no finishing kernel is launched
+    const bool swiglu_whole = epi == VX_EPI_SWIGLU && nt == 1 && p.MT <= env_int("VX_QMM_SWIGLU_MT", 3) &&
+                              p.MT != 2 && 2 * items >= cus;
     if (swiglu_whole) splits = 1;
     splits = env_int("VX_QMM_SPLITS", splits);
     splits = std::max(1, std::min(splits, S));
