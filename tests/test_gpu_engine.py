@@ -65,6 +65,33 @@ def test_forward_matches_oracle(cuda):
     assert_allclose_elementwise("verify logits", got, ref, 1e-2, 1e-2)
 
 
+def test_fused_qkv_attention_is_bit_exact(cuda, monkeypatch):
+    """Attention forming q/k/v from the qkv partials (one query tile per
+    sequence) gives the same bits as the separate norm/RoPE/scatter kernel:
+    a prefill that writes the KV pages, then a 5-row verify forward over a
+    batch of three sequences that reads them."""
+    from velox_amd import engine, synth
+
+    cfg = synth.tiny_config()
+    w = synth.host_weights(cfg, 3)
+    rng = np.random.default_rng(5)
+    outs = []
+    for fused in (False, True):
+        monkeypatch.setenv("VX_FUSED_QKV", "1" if fused else "0")
+        m = engine.PagedQwen3(cfg, w)
+        pg = engine.PagedKvCache(cfg["layers"], cfg["n_kv_heads"], cfg["head_dim"], 16, 32)
+        bts = [pg.alloc(3) for _ in range(3)]
+        r = np.random.default_rng(11)
+        lens = [9, 14, 3]
+        prompt = np.concatenate([r.integers(0, cfg["vocab"], size=n) for n in lens]).astype(np.uint32)
+        first = m.forward(pg, prompt, [(n, 0, bt) for n, bt in zip(lens, bts)]).cpu()
+        nxt = r.integers(0, cfg["vocab"], size=15).astype(np.uint32)
+        ver = m.forward_all(pg, nxt, [(5, n, bt) for n, bt in zip(lens, bts)]).cpu()
+        outs.append((first, ver))
+    assert torch.equal(outs[0][0], outs[1][0]), "prefill logits differ between fused and separate q/k/v finish"
+    assert torch.equal(outs[0][1], outs[1][1]), "verify logits differ between fused and separate q/k/v finish"
+
+
 def test_forward_tree_matches_oracle(cuda):
     from velox_amd import synth
 

@@ -31,6 +31,7 @@ namespace {
 constexpr int kKeyBlock = 64;
 constexpr int kAttnWaves = 4;  // waves per workgroup, splitting an item's key blocks
 constexpr size_t kAttnCounterBytes = 65536;
+constexpr int kMaxQkvSplits = 8;  // split partials the fused qkv finish reads
 
 struct AttnArgs {
     const void *q;
@@ -43,12 +44,23 @@ struct AttnArgs {
     void *out;
     float *partial;
     int mode;  // 0: varlen rows (cu_seqlens), 1: decode (row i = seq i)
-    int n_seqs, max_blocks, num_pages, h_q, h_kv, G, D, ps;
+    int n_seqs, n_rows, max_blocks, num_pages, h_q, h_kv, G, D, ps;
     int qr;      // query rows per tile
     int n_qtiles, n_splits, chunk;  // keys per split
     float scale_log2;               // scale * log2(e)
     uint32_t window;
     int out_bf16_round;  // round the output to bf16 before the 16-bit store
+    // Fused qkv finish (mode 0, one query tile per sequence): with qkv set,
+    // the query vectors and the sequence's new K/V rows are formed here from
+    // the qkv projection's f32 split partials [qkv_splits][total_q][N] --
+    // per-head RMSNorm (q_norm / k_norm), RoPE at rope_pos[row], K and V
+    // written into the pools at (new_pages[row], new_slots[row]) -- with the
+    // arithmetic of qk_rope_scatter_kernel<true>, instead of reading q.
+    const float *qkv;
+    int qkv_splits;
+    const uint16_t *qn_w, *kn_w, *cos_t, *sin_t;  // bf16
+    const uint32_t *rope_pos, *new_pages, *new_slots;
+    float eps;
 };
 
 template <int KT>
@@ -130,6 +142,106 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     const int k_lo = split * a.chunk;
     const int k_hi = min(kv_end, k_lo + a.chunk);
 
+    // ---- fused qkv finish: query vectors into LDS (qbuf[n][D]), this
+    // split's new K/V rows into the pools.  One wave per vector; a wave takes
+    // its vectors kVB at a time and requests every split partial of the
+    // batch before summing, so a batch costs one memory round trip.
+    if (a.qkv) {
+        constexpr int kVB = 8;
+        constexpr int kPairs = (D / 2 + 63) / 64;  // RoPE pairs per lane
+        constexpr int kE = 2 * kPairs;             // elements per lane and vector
+        uint16_t *qbuf = (uint16_t *)smem;
+        for (int i = threadIdx.x; i < (QT * 16 - nq) * D; i += 64 * kAttnWaves) qbuf[nq * D + i] = 0;
+        const int t_a = max(0, k_lo - off), t_b = min(r_seq, k_hi - off);
+        const int nkv = max(0, t_b - t_a);
+        const int nvec = nq + 2 * nkv;
+        const int QW = a.h_q * D, KW = a.h_kv * D, N = QW + 2 * KW;
+        const int half = D / 2;
+        for (int b0 = 0; b0 < nvec; b0 += kAttnWaves * kVB) {
+            float pv[kVB][kE][kMaxQkvSplits];
+            int kind[kVB], row[kVB], c0[kVB];
+            // per-vector metadata and per-lane norm weights / RoPE factors,
+            // requested with the partials (not inside the arithmetic below)
+            int64_t kv_at[kVB];
+            float wn[kVB][kE], cs[kVB][kPairs], sn[kVB][kPairs];
+#pragma unroll
+            for (int k = 0; k < kVB; k++) {
+                const int vi = b0 + wave + kAttnWaves * k;
+                kind[k] = vi >= nvec ? 3 : (vi < nq ? 0 : (vi < nq + nkv ? 1 : 2));  // q, k, v, none
+                const int t = kind[k] == 0 ? t0 + vi / a.G
+                                           : t_a + (kind[k] == 1 ? vi - nq : (kind[k] == 2 ? vi - nq - nkv : 0));
+                row[k] = row0 + t;
+                c0[k] = kind[k] == 0 ? (hk * a.G + vi % a.G) * D
+                                     : (kind[k] == 1 ? QW + hk * D : (kind[k] == 2 ? QW + KW + hk * D : 0));
+                const int rr = kind[k] == 3 ? row0 : row[k];
+                kv_at[k] = (((int64_t)a.new_pages[rr] * a.h_kv + hk) * a.ps + a.new_slots[rr]) * D;
+                const uint32_t pos = a.rope_pos[rr];
+                const uint16_t *nw = kind[k] == 0 ? a.qn_w : a.kn_w;
+#pragma unroll
+                for (int p = 0; p < kPairs; p++) {
+                    const int j = min(lane + 64 * p, half - 1);
+                    wn[k][p] = bf16_bits_to_f32(nw[j]);
+                    wn[k][kPairs + p] = bf16_bits_to_f32(nw[j + half]);
+                    cs[k][p] = bf16_bits_to_f32(a.cos_t[(int64_t)pos * half + j]);
+                    sn[k][p] = bf16_bits_to_f32(a.sin_t[(int64_t)pos * half + j]);
+                }
+#pragma unroll
+                for (int e = 0; e < kE; e++) {
+                    // q/k: element j (e < kPairs) or j + D/2; v: element lane + 64 e
+                    const int j = lane + 64 * (e % kPairs);
+                    const int c = kind[k] == 2 ? lane + 64 * e : (e < kPairs ? j : j + half);
+                    const bool ok = kind[k] < 3 && (kind[k] == 2 ? c < D : j < half);
+#pragma unroll
+                    for (int sp = 0; sp < kMaxQkvSplits; sp++)
+                        pv[k][e][sp] = (ok && sp < a.qkv_splits)
+                                           ? a.qkv[((int64_t)sp * a.n_rows + row[k]) * N + c0[k] + c] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kVB; k++) {
+                if (kind[k] == 3) continue;
+                float x[kE];
+#pragma unroll
+                for (int e = 0; e < kE; e++) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int sp = 0; sp < kMaxQkvSplits; sp++)
+                        if (sp < a.qkv_splits) acc += pv[k][e][sp];
+                    x[e] = round_to<VX_BF16>(acc);
+                }
+                if (kind[k] == 2) {
+#pragma unroll
+                    for (int e = 0; e < kE; e++)
+                        if (lane + 64 * e < D) ((uint16_t *)a.v)[kv_at[k] + lane + 64 * e] = MfmaT<KT>::cvt(x[e]);
+                    continue;
+                }
+                float ss = 0.f;
+#pragma unroll
+                for (int p = 0; p < kPairs; p++) {
+                    ss += x[p] * x[p];
+                    ss += x[kPairs + p] * x[kPairs + p];
+                }
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+                const float m = sqrtf(ss / (float)D + a.eps);
+                uint16_t *dst = kind[k] == 0 ? qbuf + (int64_t)(b0 + wave + kAttnWaves * k) * D : (uint16_t *)a.k + kv_at[k];
+#pragma unroll
+                for (int p = 0; p < kPairs; p++) {
+                    const int j = lane + 64 * p;
+                    if (j >= half) break;
+                    const float av = round_to<VX_BF16>(x[p] / m * wn[k][p]);
+                    const float bv = round_to<VX_BF16>(x[kPairs + p] / m * wn[k][kPairs + p]);
+                    const float y1 = round_to<VX_BF16>(__fsub_rn(__fmul_rn(av, cs[k][p]), __fmul_rn(bv, sn[k][p])));
+                    const float y2 = round_to<VX_BF16>(__fadd_rn(__fmul_rn(av, sn[k][p]), __fmul_rn(bv, cs[k][p])));
+                    dst[j] = MfmaT<KT>::cvt(y1);
+                    dst[j + half] = MfmaT<KT>::cvt(y2);
+                }
+            }
+        }
+        // the new K/V rows and qbuf are read by every wave below
+        __syncthreads();
+    }
+
     // ---- Q^T fragments: query n = 16*qt + lq; row t0 + n / G, head hk*G + n % G
     frag qf[QT][DK];
     int q_row[QT];
@@ -147,11 +259,15 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < DK; ks++) {
             uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-            if (live)
+            if (a.qkv)
+                raw = *(const uint4 *)((const uint16_t *)smem + n * D + ks * 32 + lg * 8);
+            else if (live)
                 raw = *(const uint4 *)((const uint16_t *)a.q + ((int64_t)(row0 + t) * a.h_q + hq) * D + ks * 32 + lg * 8);
             qf[qt][ks] = __builtin_bit_cast(frag, raw);
         }
     }
+    // qbuf shares LDS with the V^T tiles of the key loop
+    if (a.qkv) __syncthreads();
 
     floatx4 o[DT][QT];
 #pragma unroll
@@ -531,9 +647,22 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
                            int64_t max_blocks, int64_t num_pages, int64_t h_q, int64_t h_kv,
                            int64_t D, int64_t ps, float scale, uint32_t window, int dtype,
                            void *workspace, size_t ws_bytes, int64_t max_kv, hipStream_t st,
-                           int out_bf16_round) {
+                           int out_bf16_round, const AttnQkvFuse *fuse) {
     AttnArgs a{};
     a.out_bf16_round = out_bf16_round;
+    a.n_rows = (int)total_q;
+    if (fuse) {
+        a.qkv = fuse->partial;
+        a.qkv_splits = fuse->splits;
+        a.qn_w = fuse->qn;
+        a.kn_w = fuse->kn;
+        a.cos_t = fuse->cos_t;
+        a.sin_t = fuse->sin_t;
+        a.rope_pos = fuse->pos;
+        a.new_pages = fuse->pages;
+        a.new_slots = fuse->slots;
+        a.eps = fuse->eps;
+    }
     a.q = q;
     a.k = k_pool;
     a.v = v_pool;
@@ -567,6 +696,9 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
     if (QT == 3) QT = 4;
     a.qr = std::max(1, (QT * 16) / a.G);
     a.n_qtiles = (int)vx_cdiv(max_rows, a.qr);
+    if (fuse && (mode != 0 || a.n_qtiles != 1 || dtype == VX_F32 || fuse->splits < 1 || fuse->splits > kMaxQkvSplits))
+        return set_error("paged_attention: the fused qkv finish needs one query tile per sequence (mode 0, 16-bit) "
+                         "and at most 8 qkv splits");
     // KV split across workgroups (each workgroup's four waves already split
     // its range): aim for ~2 workgroups per CU, at least one key block per wave
     const int64_t base_items = n_seqs * h_kv * a.n_qtiles;
@@ -634,7 +766,7 @@ extern "C" int vx_paged_attention(const void *q, const void *k_pool, const void 
     return paged_attention_launch(q, k_pool, v_pool, block_table, cu_seqlens, kv_offsets, tree_mask,
                                   out, 0, total_q, n_seqs, total_q, max_blocks, num_pages, h_q, h_kv,
                                   head_dim, page_size, scale, sliding_window, dtype, nullptr, 0,
-                                  max_blocks * page_size, (hipStream_t)stream, 0);
+                                  max_blocks * page_size, (hipStream_t)stream, 0, nullptr);
 }
 
 extern "C" int vx_paged_decode_attention(const void *q, const void *k_pool, const void *v_pool,
@@ -649,5 +781,5 @@ extern "C" int vx_paged_decode_attention(const void *q, const void *k_pool, cons
     return paged_attention_launch(q, k_pool, v_pool, block_table, nullptr, kv_lens, nullptr, out, 1, n, n,
                                   1, max_blocks, num_pages, h_q, h_kv, head_dim, page_size, scale,
                                   sliding_window, dtype, nullptr, 0, max_blocks * page_size,
-                                  (hipStream_t)stream, 0);
+                                  (hipStream_t)stream, 0, nullptr);
 }

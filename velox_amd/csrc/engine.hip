@@ -101,7 +101,7 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
                            int64_t max_blocks, int64_t num_pages, int64_t h_q, int64_t h_kv,
                            int64_t D, int64_t ps, float scale, uint32_t window, int dtype,
                            void *workspace, size_t ws_bytes, int64_t max_kv, hipStream_t st,
-                           int out_bf16_round);
+                           int out_bf16_round, const AttnQkvFuse *fuse);
 size_t accept_workspace_bytes(int64_t rows, int64_t vocab);
 size_t stochastic_workspace_bytes(int64_t rows, int64_t vocab);
 int argmax_accept_launch(const void *logits, int ldt, int64_t rows, int64_t vocab, int mode,
@@ -645,6 +645,13 @@ int ensure_buffers(vx_model *m, int64_t rows) {
     return 0;
 }
 
+// The attention launch of a layer may read the qkv projection's split
+// partials (fused finish) while it writes its own split partials: its
+// workspace starts past them.
+size_t attn_ws_offset(int64_t rows, int64_t N, int64_t K) {
+    return (qmm_partial_ws_bytes(rows, N, K) + 255) & ~(size_t)255;
+}
+
 size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int64_t n_seqs, int64_t max_rows,
                         int64_t max_kv) {
     const vx_qwen3_config &c = m->cfg;
@@ -663,7 +670,8 @@ size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int
     const int64_t qr = std::max<int64_t>(1, qt * 16 / G);
     const int64_t nqt = vx_cdiv(max_rows, qr);
     const int64_t splits = std::max<int64_t>(1, vx_cdiv(max_kv, 128));
-    need = std::max(need, attn_workspace_bytes(n_seqs, c.n_kv_heads, nqt, splits, c.head_dim));
+    need = std::max(need, attn_ws_offset(rows, QW + 2 * KW, H) +
+                              attn_workspace_bytes(n_seqs, c.n_kv_heads, nqt, splits, c.head_dim));
     return need;
 }
 
@@ -705,6 +713,15 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     }
     int splits = 0;
     const float *part = nullptr;
+    // Opt-in (VX_FUSED_QKV=1): with one query tile per sequence (up to 64
+    // query vectors for head_dim <= 128, 32 above) attention can finish
+    // q/k/v itself.  It is bit-identical to the separate kernel but measured
+    // slower at the bench shape (27.7 us against 5.4 + 11.0 us): the
+    // finish adds four dependent memory round trips ahead of the key loop on
+    // 128 workgroups, where the separate kernel spreads them over the chip.
+    const int64_t G = HQ / HK;
+    const char *fz_env = getenv("VX_FUSED_QKV");
+    const bool fuse_qkv = meta.max_rows * G <= (D <= 128 ? 64 : 32) && fz_env && atoi(fz_env) != 0;
     for (int64_t l = 0; l < m->L; l++) {
         const LayerDev &ly = m->layers[l];
         uint16_t *kp = (uint16_t *)vx_pages_pool(pg, l, 0);
@@ -713,17 +730,26 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, QW + 2 * KW, H, false));
             VX_TRY(qmm_packed_partial(xn, ly.qkv.packed, R, QW + 2 * KW, H, ws, ws_bytes, &splits, &part, st));
         }
-        {
-            ProfScope ps_(prof, st, PC_OTHER, 0.0);
-            VX_TRY(qkv_partial_rope_scatter_launch(part, splits, ly.qn, ly.kn, m->cos_t, m->sin_t, pos, pages, slots,
-                                                   q, kp, vp, R, (int)HQ, (int)HK, (int)D, (int)pg->page_size, eps,
-                                                   VX_F16, st));
-        }
-        {
+        if (fuse_qkv) {
+            // q/k norm, RoPE and the KV write happen inside the attention launch
+            const AttnQkvFuse fz{part, splits, ly.qn, ly.kn, m->cos_t, m->sin_t, pos, pages, slots, eps};
+            const size_t off = attn_ws_offset(R, QW + 2 * KW, H);
+            ProfScope ps_(prof, st, PC_ATTN, kv_bytes_per_layer + 4.0 * R * QW);
+            VX_TRY(paged_attention_launch(nullptr, kp, vp, bt, cu, kvo, mask, attn, 0, R, meta.n_seqs,
+                                          meta.max_rows, meta.max_blocks, pg->num_pages, HQ, HK, D, pg->page_size,
+                                          scale, 0, VX_F16, (char *)ws + off, ws_bytes - off, meta.max_kv, st, 1,
+                                          &fz));
+        } else {
+            {
+                ProfScope ps_(prof, st, PC_OTHER, 0.0);
+                VX_TRY(qkv_partial_rope_scatter_launch(part, splits, ly.qn, ly.kn, m->cos_t, m->sin_t, pos, pages,
+                                                       slots, q, kp, vp, R, (int)HQ, (int)HK, (int)D,
+                                                       (int)pg->page_size, eps, VX_F16, st));
+            }
             ProfScope ps_(prof, st, PC_ATTN, kv_bytes_per_layer + 4.0 * R * QW);
             VX_TRY(paged_attention_launch(q, kp, vp, bt, cu, kvo, mask, attn, 0, R, meta.n_seqs, meta.max_rows,
                                           meta.max_blocks, pg->num_pages, HQ, HK, D, pg->page_size, scale, 0,
-                                          VX_F16, ws, ws_bytes, meta.max_kv, st, 1));
+                                          VX_F16, ws, ws_bytes, meta.max_kv, st, 1, nullptr));
         }
         {
             ProfScope ps_(prof, st, PC_QMM, qmm_bytes(R, H, QW, true));

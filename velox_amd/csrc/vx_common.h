@@ -169,4 +169,15 @@ int device_cu_count();
 // the first `zero_bytes` of it are kept zero between launches by the kernels
 // that use them as counters.
 int stream_workspace(hipStream_t s, size_t bytes, void **out);
+
+// The qkv projection's split partials and what finishing them needs (per-head
+// norm weights, RoPE tables and positions, KV destinations), handed to the
+// attention launcher when it forms q, K and V itself.
+struct AttnQkvFuse {
+    const float *partial;  // [splits][rows][(h_q + 2 h_kv) * D]
+    int splits;
+    const uint16_t *qn, *kn, *cos_t, *sin_t;
+    const uint32_t *pos, *pages, *slots;
+    float eps;
+};
 }  // namespace vx
