@@ -222,6 +222,20 @@ int vx_model_create(const vx_qwen3_config *cfg, const vx_weights_host *w, int64_
 void vx_model_destroy(vx_model *m);
 
 /* SeqSlice (qwen3.rs:254-263): block_table is a host array. */
+/* Tree-path KV compaction.  No counterpart in the reference (its spec loop
+ * is a chain); tree verification (vx_forward with tree_parents) writes node j
+ * of each sequence at position kv_offset + j, and after vx_accept_tree the
+ * accepted path must sit at consecutive positions: for d = 1..accepted[b],
+ * position kv_offsets[b] + d receives, in every layer, K and V and kv head,
+ * the row of node path[b, d] (position kv_offsets[b] + path[b, d]); the root
+ * (d = 0) stays.  Every destination receives its source's value from before
+ * the call.  block_tables [n_seqs, max_blocks] u32, kv_offsets [n_seqs] u32,
+ * accepted [n_seqs] i32, path [n_seqs, r] i32: device arrays, as
+ * vx_accept_tree writes them.  r <= 64. */
+int vx_kv_compact_path(vx_pages *pages, const uint32_t *block_tables, int64_t max_blocks,
+                       const uint32_t *kv_offsets, const int32_t *accepted, const int32_t *path,
+                       int64_t n_seqs, int64_t r, void *stream);
+
 typedef struct {
     int64_t new_tokens, kv_offset;
     const uint32_t *block_table;

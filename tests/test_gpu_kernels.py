@@ -483,3 +483,49 @@ def test_accept_tree_exact(cuda):
         a = ra[b]
         assert np.array_equal(path.cpu().numpy()[b, : a + 1], rp[b, : a + 1])
         assert np.array_equal(tok.cpu().numpy().view(np.uint32)[b, : a + 1], rt[b, : a + 1])
+
+
+def _pool_copy(dst_ptr, src_ptr, nbytes):
+    import ctypes as C
+
+    rt = C.CDLL("libamdhip64.so.7")
+    rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    assert rt.hipMemcpy(dst_ptr, src_ptr, nbytes, 3) == 0  # device to device
+
+
+def test_kv_compact_path(cuda):
+    """Tree-path compaction: positions kv_offset + d take the rows of node
+    path[d] (read before any move) in every layer, K/V and head; other rows
+    are untouched.  Shuffled pages, a path crossing a page boundary, a
+    sequence with nothing accepted."""
+    from velox_amd import engine, ops
+
+    L, HK, D, ps, P = 2, 2, 64, 16, 12
+    pg = engine.PagedKvCache(L, HK, D, ps, P)
+    rng = np.random.default_rng(4)
+    pool_elems = P * HK * ps * D
+    pools = [rng.standard_normal(pool_elems).astype(np.float16) for _ in range(2 * L)]
+    for i, arr in enumerate(pools):
+        t = torch.from_numpy(arr).cuda()
+        _pool_copy(pg.layer_pool_ptr(i // 2, i % 2), t.data_ptr(), t.numel() * 2)
+    torch.cuda.synchronize()
+    bt = np.array([[7, 2], [0, 11], [5, 9]], np.uint32)
+    kvo = np.array([3, 10, 12], np.uint32)
+    r = 7
+    paths = np.zeros((3, r), np.int32)
+    paths[0, :4] = [0, 1, 3, 6]
+    paths[2, :3] = [0, 2, 5]
+    acc = np.array([3, 0, 2], np.int32)
+    ops.kv_compact_path(pg, u32(bt), u32(kvo), torch.from_numpy(acc).cuda(), torch.from_numpy(paths).cuda())
+    torch.cuda.synchronize()
+    for i, arr in enumerate(pools):
+        want = arr.reshape(P, HK, ps, D).copy()
+        src = arr.reshape(P, HK, ps, D)
+        for b in range(3):
+            for d in range(1, acc[b] + 1):
+                sp, dp = int(kvo[b]) + int(paths[b, d]), int(kvo[b]) + d
+                want[bt[b, dp // ps], :, dp % ps] = src[bt[b, sp // ps], :, sp % ps]
+        got = torch.empty(pool_elems, dtype=torch.float16, device="cuda")
+        _pool_copy(got.data_ptr(), pg.layer_pool_ptr(i // 2, i % 2), pool_elems * 2)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy().reshape(P, HK, ps, D), want), f"pool {i} differs"

@@ -114,6 +114,7 @@ _SIGS = {
     "vx_pages_num_free": (i64, [vp]),
     "vx_pages_refcount": (C.c_uint32, [vp, C.c_uint32]),
     "vx_pages_pool": (vp, [vp, i64, i32]),
+    "vx_kv_compact_path": (i32, [vp, vp, i64, vp, vp, vp, i64, i64, vp]),
     "vx_model_create": (i32, [C.POINTER(QwenConfig), C.POINTER(WeightsHost), i64, C.POINTER(vp)]),
     "vx_model_destroy": (None, [vp]),
     "vx_forward": (i32, [vp, vp, u32p, C.POINTER(SeqSlice), i64, i32, C.POINTER(C.c_int32), vp, vp]),

@@ -288,6 +288,66 @@ extern "C" void *vx_pages_pool(vx_pages *p, int64_t layer, int kv) {
     return (char *)p->base + (size_t)(layer * 2 + (kv ? 1 : 0)) * p->pool_bytes;
 }
 
+namespace {
+
+// Tree-path KV compaction: one workgroup per (sequence, layer x {K, V}, kv
+// head).  The accepted path's rows (node path[d] at position kv_offset +
+// path[d], d = 1..A) are first read into LDS, then written at kv_offset + d,
+// so every destination receives its source's value from before the move
+// (path[d] >= d: a destination never precedes a source still to be read in
+// sequential order either).  Rows move as raw 32-bit words.
+__global__ __launch_bounds__(256) void kv_compact_path_kernel(uint8_t *base, size_t pool_bytes, const uint32_t *bt,
+                                                              int max_blocks, const uint32_t *kv_offsets,
+                                                              const int32_t *accepted, const int32_t *path, int r,
+                                                              int kv_heads, int page_size, int num_pages,
+                                                              int row_words) {
+    extern __shared__ uint32_t rows[];
+    const int b = blockIdx.x;
+    const int pool = blockIdx.y;  // layer * 2 + (K|V)
+    const int h = blockIdx.z;
+    const int A = min(max(accepted[b], 0), r - 1);
+    const int64_t kv0 = kv_offsets[b];
+    const uint32_t *btr = bt + (int64_t)b * max_blocks;
+    uint32_t *pw = (uint32_t *)(base + (size_t)pool * pool_bytes);
+    auto row_at = [&](int64_t pos) -> int64_t {  // word offset of (pos, head h)
+        const int blk = (int)min<int64_t>(pos / page_size, max_blocks - 1);
+        const int64_t page = min<int64_t>(btr[blk], num_pages - 1);
+        return ((page * kv_heads + h) * page_size + pos % page_size) * row_words;
+    };
+    for (int i = threadIdx.x; i < A * row_words; i += blockDim.x) {
+        const int d = 1 + i / row_words;
+        const int src = min(max(path[(int64_t)b * r + d], 0), r - 1);
+        rows[i] = pw[row_at(kv0 + src) + i % row_words];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < A * row_words; i += blockDim.x) {
+        const int d = 1 + i / row_words;
+        pw[row_at(kv0 + d) + i % row_words] = rows[i];
+    }
+}
+
+}  // namespace
+
+extern "C" int vx_kv_compact_path(vx_pages *p, const uint32_t *block_tables, int64_t max_blocks,
+                                  const uint32_t *kv_offsets, const int32_t *accepted, const int32_t *path,
+                                  int64_t n_seqs, int64_t r, void *stream) {
+    VX_REQUIRE(p, "kv_compact_path: null pages");
+    VX_REQUIRE(r >= 1 && r <= 64, "kv_compact_path: tree of 1..64 nodes");
+    VX_REQUIRE(max_blocks >= 1, "kv_compact_path: empty block table");
+    if (n_seqs == 0) return 0;
+    VX_REQUIRE(block_tables && kv_offsets && accepted && path, "kv_compact_path: null tensor");
+    const int row_words = (int)(p->head_dim * 2 / 4);
+    VX_REQUIRE(p->head_dim % 2 == 0, "kv_compact_path: head_dim must be even");
+    const size_t lds = (size_t)(r - 1) * row_words * 4;
+    if (r == 1) return 0;
+    hipLaunchKernelGGL(kv_compact_path_kernel, dim3((unsigned)n_seqs, (unsigned)(p->layers * 2), (unsigned)p->kv_heads),
+                       dim3(256), lds, (hipStream_t)stream, (uint8_t *)p->base, p->pool_bytes, block_tables,
+                       (int)max_blocks, kv_offsets, accepted, path, (int)r, (int)p->kv_heads, (int)p->page_size,
+                       (int)p->num_pages, row_words);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
 // ===========================================================================
 // model (qwen3.rs)
 // ===========================================================================

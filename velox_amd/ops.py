@@ -209,6 +209,20 @@ def sample_rows(logits, uniforms, temperature, uniform_stride=1):
     return out
 
 
+def kv_compact_path(pages, block_tables, kv_offsets, accepted, path):
+    """Move each sequence's accepted tree path to consecutive KV positions
+    (vx_kv_compact_path): pages is an engine.PagedKvCache; block_tables
+    uint32 [B, max_blocks], kv_offsets uint32 [B], accepted int32 [B] and
+    path int32 [B, r] are device tensors (accepted / path as accept_tree
+    returns them)."""
+    b, mb = block_tables.shape
+    _need(path.dim() == 2 and path.shape[0] == b and accepted.shape[0] == b and kv_offsets.shape[0] == b,
+          "kv_compact_path: shape mismatch")
+    _contig("kv_compact_path", block_tables=block_tables, kv_offsets=kv_offsets, accepted=accepted, path=path)
+    check(lib.vx_kv_compact_path(pages._h, block_tables.data_ptr(), mb, kv_offsets.data_ptr(), accepted.data_ptr(),
+                                 path.data_ptr(), b, path.shape[1], _stream()))
+
+
 def accept_tree(logits, parents, node_tokens):
     """logits [B, R, V]; parents: host ints (parents[0] = -1); node_tokens [B, R]."""
     import ctypes as C
