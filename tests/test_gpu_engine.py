@@ -229,3 +229,25 @@ def test_config0_qwen3_0_6b_shape(cuda):
     prompt = synth.prompt(0, 8, cfg["vocab"])
     r, *_ = run_greedy_pair(cfg, 0, 4, [prompt], k=4, rounds=3)
     assert r >= 1
+
+
+def test_mlx_checkpoint_loads_and_runs(cuda, tmp_path):
+    """A checkpoint in the MLX int4 on-disk format (written with safetensors,
+    sharded) loads through velox_amd.loader into the GPU engine, whose
+    forward matches the oracle run on the same loaded weights."""
+    from test_loader import write_checkpoint
+    from velox_amd import engine, loader, synth
+
+    cfg = synth.tiny_config(layers=2)
+    write_checkpoint(tmp_path, cfg, synth.host_weights(cfg, 6))
+    lcfg, w = loader.load_mlx_qwen3(str(tmp_path))
+    lcfg.pop("tie_word_embeddings")
+    g = engine.PagedQwen3(lcfg, w)
+    o = vxo.Model(dict(lcfg, dtype=vxo.BF16), synth.as_model_dtype(w, "bf16"), threads=8)
+    gp = engine.PagedKvCache(lcfg["layers"], lcfg["n_kv_heads"], lcfg["head_dim"], 16, 8)
+    op = vxo.Pages(lcfg["layers"], lcfg["n_kv_heads"], lcfg["head_dim"], 16, 8)
+    prompt = np.random.default_rng(2).integers(0, lcfg["vocab"], size=9).astype(np.uint32)
+    gbt, obt = gp.alloc(1), op.alloc(1)
+    got = g.forward_all(gp, prompt, [(9, 0, gbt)]).float().cpu().numpy()
+    ref = vxo.forward(o, op, prompt, [(9, 0, obt)], all_rows=True)
+    assert_allclose_elementwise("loaded checkpoint logits", got, ref, 1e-2, 1e-2)
