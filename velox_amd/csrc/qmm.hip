@@ -1434,11 +1434,11 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     int nt = env_int("VX_QMM_NT", 1);
     p.NT = nt;
     p.P = p32_depth(p.MT, nt);
-    // the eight-wave kernel for one row tile (draft rows) below LM-head
-    // widths; for three row tiles it is chosen below when the K range per
-    // workgroup is short
+    // the eight-wave kernel for three row tiles (verify rows) and for one row
+    // tile below LM-head widths (measured in the spec bench: the four-wave
+    // kernel is faster only for the draft's one-row-tile LM head)
     const int k2_env = env_int("VX_QMM_K2", -1);
-    p.k2 = k2_env >= 0 ? k2_env != 0 : (p.MT == 1 && N <= 65536 && nt == 1);
+    p.k2 = k2_env >= 0 ? k2_env != 0 : (nt == 1 && (p.MT == 3 || (p.MT == 1 && N <= 65536)));
     p.col_blocks = (int)vx_cdiv(N, kWaves * nt * 32);
     const int items = p.col_blocks * p.m_blocks;
     // three row tiles hold one workgroup per CU (registers); fewer hold two.
@@ -1464,7 +1464,6 @@ Plan make_plan_p32(int64_t M, int64_t N, int64_t K, int epi) {
     p.splits = splits;
     p.sps = sps;
     p.gps = 2 * sps;
-    if (k2_env < 0 && p.MT == 3 && nt == 1 && (sps <= 4 || swiglu_whole)) p.k2 = true;
     p.total_items = p.col_blocks * p.splits;
     p.per_xcd = (int)vx_cdiv(p.total_items, 8);
     p.partial_bytes = (p.splits > 1 || epi == kEpiPartial) ? (size_t)p.splits * M * N * 4 : 0;
