@@ -962,6 +962,21 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
 }
 
+// vm_wait<steps * (live + UW)> for a wave-uniform live count 0..UX (UX <= 3)
+template <int STEPS, int UX, int UW>
+__device__ __forceinline__ void vm_wait_live(int live) {
+    static_assert(UX <= 3, "up to three DMA instructions per wave and step");
+    if (live >= UX) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(STEPS * (UX + UW)));
+    } else if (UX >= 2 && live == UX - 1) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(STEPS * (UX - 1 + UW)));
+    } else if (UX >= 3 && live == UX - 2) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(STEPS * (UX - 2 + UW)));
+    } else {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(STEPS * UW));
+    }
+}
+
 template <int N>
 __device__ __forceinline__ void vm_wait() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -1188,6 +1203,10 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
 #pragma unroll
         for (int g = 0; g < UX; g++) xoff[g] = min(m0 + 32 * g + rl, a.M - 1) * a.K + 8 * c;
     }
+    // DMA instructions whose four rows all lie past M are skipped (those LDS
+    // rows only feed accumulator rows that are never stored); the count of
+    // live ones is wave-uniform and selects the step's vmcnt immediate
+    const int nx = min(UX, max(0, (a.M - m0 - 4 * wave + 31) / 32));
     const uint32_t xs_addr = (uint32_t)(uintptr_t)(lds_void_t *)xs;
     const uint32_t xs_wave = __builtin_amdgcn_readfirstlane(xs_addr + wave * 64 * 16);
     // fragment (j, t), j = 4 kh + jj: byte 8192 t + (xrd ^ 32 j)
@@ -1217,7 +1236,8 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
 
     auto issue = [&](int st, int buf, uint4 (&w)[NT], uint32_t (&sv)[NT]) {
 #pragma unroll
-        for (int g = 0; g < UX; g++) dma16(xh + xoff[g] + st * 128, xs_wave + (uint32_t)(buf * BUF + 512 * g) * 16);
+        for (int g = 0; g < UX; g++)
+            if (g < nx) dma16(xh + xoff[g] + st * 128, xs_wave + (uint32_t)(buf * BUF + 512 * g) * 16);
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const uint8_t *bp = wblk[nt] + (int64_t)st * kPackBlock;
@@ -1228,7 +1248,7 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     auto step = [&](int st, auto slot_c) {
         constexpr int I = decltype(slot_c)::value;
         constexpr int NX = (I + P) % R;
-        vm_wait<VM>();
+        vm_wait_live<P - 1, UX, UW>(nx);
         __builtin_amdgcn_s_barrier();
         issue(min(st + P, s_hi - 1), NX, wq[NX], sb[NX]);
         __builtin_amdgcn_sched_barrier(0);
