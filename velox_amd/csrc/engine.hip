@@ -127,6 +127,12 @@ int qkv_partial_rope_scatter_launch(const float *partial, int splits, const uint
                                     hipStream_t st);
 int residual_rmsnorm_launch(const float *partial, int splits, float acc_scale, uint16_t *h, const uint16_t *ln,
                             uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
+bool qmm_packed_argmax_ok(int64_t M, int64_t N, int64_t K);
+int qmm_packed_argmax(const void *x, const void *packed, void *y, int64_t M, int64_t N, int64_t K, int round_dt,
+                      int y_dt, float *amax_v, uint32_t *amax_i, void *workspace, size_t ws_bytes, hipStream_t st);
+int argmax_accept_partials_launch(const float *pv, const uint32_t *pi, int n_chunks, int64_t rows, int mode,
+                                  int rows_per_group, const uint32_t *cand, int k, int32_t *accepted,
+                                  uint32_t *tokens, uint32_t *next_ids, int64_t next_stride, hipStream_t st);
 size_t qmm_partial_ws_bytes(int64_t M, int64_t N, int64_t K);
 int qmm_packed_partial(const void *x, const void *packed, int64_t M, int64_t N, int64_t K, void *workspace,
                        size_t ws_bytes, int *splits, const float **partial, hipStream_t st);
@@ -736,9 +742,13 @@ size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int
 }
 
 // Forward over `rows` rows whose token ids are already on the device.
+// With amax_v set, the LM head also writes greedy-argmax partials of its
+// logits ([rows, vocab / 128]) and *amax_done reports whether it did.
 int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &meta, const uint8_t *meta_dev,
                 int all_rows, void *logits, void *ws, size_t ws_bytes, hipStream_t st, Prof *prof = nullptr,
-                double kv_bytes_per_layer = 0.0) {
+                double kv_bytes_per_layer = 0.0, float *amax_v = nullptr, uint32_t *amax_i = nullptr,
+                bool *amax_done = nullptr) {
+    if (amax_done) *amax_done = false;
     const vx_qwen3_config &c = m->cfg;
     const int64_t H = c.hidden, F = c.inter, D = c.head_dim, HQ = c.n_heads, HK = c.n_kv_heads;
     const int64_t QW = HQ * D, KW = HK * D, R = meta.rows;
@@ -843,8 +853,14 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     }
     {
         ProfScope ps_(prof, st, PC_QMM, qmm_bytes(lrows, c.vocab, H, false));
-        VX_TRY(qmm_packed(xn, m->lm.packed, logits, nullptr, lrows, c.vocab, H, 0, 0, VX_BF16,
-                               VX_BF16, VX_EPI_STORE, ws, ws_bytes, st));
+        if (amax_v && qmm_packed_argmax_ok(lrows, c.vocab, H)) {
+            VX_TRY(qmm_packed_argmax(xn, m->lm.packed, logits, lrows, c.vocab, H, VX_BF16, VX_BF16, amax_v, amax_i,
+                                     ws, ws_bytes, st));
+            if (amax_done) *amax_done = true;
+        } else {
+            VX_TRY(qmm_packed(xn, m->lm.packed, logits, nullptr, lrows, c.vocab, H, 0, 0, VX_BF16, VX_BF16,
+                              VX_EPI_STORE, ws, ws_bytes, st));
+        }
     }
     return 0;
 }
@@ -910,6 +926,7 @@ struct vx_spec {
     std::vector<SpecState> states;
     // device buffers for a round
     DevBuf d_ids, d_cand, d_vids, d_tlog, d_dlog, d_acc, d_tok, d_uni, d_meta, d_argws, d_draw;
+    DevBuf d_amax;  // greedy-argmax partials written by the LM heads: values then indices
     // host staging (pinned)
     void *h_stage = nullptr;
     size_t h_stage_n = 0;
@@ -1110,6 +1127,10 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     VX_TRY(e->d_tok.ensure(n * (D + 1) * 4));
     VX_TRY(e->d_uni.ensure(n * (D + 1) * 16));
     VX_TRY(e->d_draw.ensure(n * 4));
+    const int64_t amax_chunks = vx_cdiv(V, 128);
+    VX_TRY(e->d_amax.ensure((size_t)n * (D + 1) * amax_chunks * 8));
+    float *amax_v = (float *)e->d_amax.p;
+    uint32_t *amax_i = (uint32_t *)(amax_v + n * (D + 1) * amax_chunks);
     size_t accws = std::max(accept_workspace_bytes(n * (D + 1), V), stochastic_workspace_bytes(n * (2 * D + 1), V));
     if (e->d_argws.n < accws) {
         VX_HIP(hipDeviceSynchronize());
@@ -1148,9 +1169,13 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     // ---- draft phase: feed [last, c0 .. c_{D-2}] (spec.rs:223-240)
     for (int64_t i = 0; i < D; i++) {
         void *dl = stoch ? (void *)((uint16_t *)e->d_dlog.p + (size_t)i * n * V) : e->d_dlog.p;
+        bool fused_amax = false;
         VX_TRY(forward_dev(e->draft, e->dp, ids, metas[i], dm + boff[i], 0, dl, e->draft->ws.p, e->draft->ws.n, st,
-                           prof ? &e->prof_draft : nullptr, kv_draft));
-        if (!stoch) {
+                           prof ? &e->prof_draft : nullptr, kv_draft, stoch ? nullptr : amax_v, amax_i, &fused_amax));
+        if (!stoch && fused_amax) {
+            VX_TRY(argmax_accept_partials_launch(amax_v, amax_i, (int)amax_chunks, n, 0, 1, nullptr, 0, nullptr,
+                                                 nullptr, cand + i, D, st));
+        } else if (!stoch) {
             VX_TRY(argmax_accept_launch(dl, VX_BF16, n, V, 0, 1, nullptr, 0, nullptr, nullptr, nullptr, nullptr,
                                         nullptr, cand + i, D, e->d_argws.p, e->d_argws.n, st));
         } else {
@@ -1165,11 +1190,16 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
                        (uint32_t *)e->d_vids.p, n, D);
     VX_HIP(hipGetLastError());
     if (prof) VX_HIP(hipEventRecord(e->ev[1], st));
+    bool verify_amax = false;
     VX_TRY(forward_dev(e->target, e->tp, (const uint32_t *)e->d_vids.p, metas[D], dm + boff[D], 1, e->d_tlog.p,
-                       e->target->ws.p, e->target->ws.n, st, prof ? &e->prof_verify : nullptr, kv_verify));
+                       e->target->ws.p, e->target->ws.n, st, prof ? &e->prof_verify : nullptr, kv_verify,
+                       stoch ? nullptr : amax_v, amax_i, &verify_amax));
     if (prof) VX_HIP(hipEventRecord(e->ev[2], st));
     // ---- acceptance (spec.rs:266-292)
-    if (!stoch) {
+    if (!stoch && verify_amax) {
+        VX_TRY(argmax_accept_partials_launch(amax_v, amax_i, (int)amax_chunks, n * (D + 1), 1, (int)(D + 1), cand,
+                                             (int)D, (int32_t *)e->d_acc.p, (uint32_t *)e->d_tok.p, nullptr, 0, st));
+    } else if (!stoch) {
         VX_TRY(argmax_accept_launch(e->d_tlog.p, VX_BF16, n * (D + 1), V, 1, (int)(D + 1), cand, (int)D,
                                     (int32_t *)e->d_acc.p, (uint32_t *)e->d_tok.p, nullptr, nullptr, nullptr, nullptr,
                                     0, e->d_argws.p, e->d_argws.n, st));

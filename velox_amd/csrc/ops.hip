@@ -346,17 +346,37 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(AcceptArgs a) {
 
 // Pass 2: one block per group (sequence): combine chunk partials of each row
 // in chunk order, then the acceptance walk on thread 0.
+// The partials never hold NaN (it never wins a chunk), so arg_better is a
+// total order on them and the 64 lanes may combine a row's chunks strided and
+// then by butterfly: the same winner as the sequential scan.
 __global__ __launch_bounds__(64) void accept_finish_kernel(AcceptArgs a) {
     __shared__ uint32_t am[64];
     const int64_t grp = blockIdx.x;
-    for (int rr = threadIdx.x; rr < a.rows_per_group; rr += blockDim.x) {
+    for (int rr = 0; rr < a.rows_per_group; rr++) {
         const int64_t rw = grp * a.rows_per_group + rr;
         ArgBest best = {-__builtin_inff(), 0xffffffffu};
-        for (int c = 0; c < a.n_chunks; c++) best = arg_better(best, {a.pv[rw * a.n_chunks + c], a.pi[rw * a.n_chunks + c]});
-        const uint32_t idx = best.i == 0xffffffffu ? 0u : best.i;
-        if (rr < 64) am[rr] = idx;
-        if (a.argmax_out) a.argmax_out[rw] = idx;
-        if (a.mode == 0 && a.next_ids) a.next_ids[rw * a.next_stride] = idx;
+        // eight partials per lane in flight per batch
+        for (int c0 = threadIdx.x; c0 < a.n_chunks; c0 += 64 * 8) {
+            float v[8];
+            uint32_t ix[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int c = c0 + 64 * u;
+                v[u] = c < a.n_chunks ? a.pv[rw * a.n_chunks + c] : -__builtin_inff();
+                ix[u] = c < a.n_chunks ? a.pi[rw * a.n_chunks + c] : 0xffffffffu;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) best = arg_better(best, {v[u], ix[u]});
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            best = arg_better(best, {__shfl_xor(best.v, o), (uint32_t)__shfl_xor((int)best.i, o)});
+        if (threadIdx.x == 0) {
+            const uint32_t idx = best.i == 0xffffffffu ? 0u : best.i;
+            am[rr] = idx;
+            if (a.argmax_out) a.argmax_out[rw] = idx;
+            if (a.mode == 0 && a.next_ids) a.next_ids[rw * a.next_stride] = idx;
+        }
     }
     __syncthreads();
     if (threadIdx.x != 0 || a.mode == 0) return;
@@ -682,6 +702,33 @@ int argmax_accept_launch(const void *logits, int ldt, int64_t rows, int64_t voca
         hipLaunchKernelGGL(argmax_partial_kernel<VX_F16>, grid, dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL(argmax_partial_kernel<VX_F32>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(accept_finish_kernel, dim3((unsigned)(rows / rows_per_group)), dim3(64), 0, st, a);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+// Greedy argmax / acceptance from (value, first index) partials that the LM
+// head's GEMM epilogue wrote ([rows, n_chunks], one per 128 columns): the
+// first pass over the logits is skipped.
+int argmax_accept_partials_launch(const float *pv, const uint32_t *pi, int n_chunks, int64_t rows, int mode,
+                                  int rows_per_group, const uint32_t *cand, int k, int32_t *accepted,
+                                  uint32_t *tokens, uint32_t *next_ids, int64_t next_stride, hipStream_t st) {
+    VX_REQUIRE(rows > 0 && n_chunks > 0, "argmax: empty partials");
+    VX_REQUIRE(rows_per_group >= 1 && rows_per_group <= 64 && rows % rows_per_group == 0,
+               "accept: rows per sequence must be 1..64");
+    VX_REQUIRE(mode == 0 || mode == 1, "accept: partials serve greedy argmax and chain acceptance");
+    AcceptArgs a{};
+    a.rows_per_group = rows_per_group;
+    a.n_chunks = n_chunks;
+    a.pv = (float *)pv;
+    a.pi = (uint32_t *)pi;
+    a.mode = mode;
+    a.cand = cand;
+    a.k = k;
+    a.accepted = accepted;
+    a.tokens = tokens;
+    a.next_ids = next_ids;
+    a.next_stride = next_stride;
     hipLaunchKernelGGL(accept_finish_kernel, dim3((unsigned)(rows / rows_per_group)), dim3(64), 0, st, a);
     VX_HIP(hipGetLastError());
     return 0;

@@ -74,6 +74,11 @@ struct QmmArgs {
     int epi, round_dt, y_dt;
     float acc_scale;    // 2^x_shift
     float store_scale;  // 2^-y_shift
+    // STORE epilogue of the packed kernels: optional greedy-argmax partials of
+    // the stored values, (value, first index) per (row, 128-column block) at
+    // [row * ceil(N/128) + block]; NaN never wins, ties keep the smaller index
+    float *amax_v;
+    uint32_t *amax_i;
 };
 
 typedef unsigned short ushort8 __attribute__((ext_vector_type(8)));
@@ -899,6 +904,7 @@ __device__ __forceinline__ void finish_rows(const QmmArgs &a, const float *lds, 
         return;
     }
     constexpr int PIECES = 4 * MT * 32 * 8;
+    const bool amax = a.amax_v != nullptr && !partial;
 #pragma unroll
     for (int k = 0; k < (PIECES + THREADS - 1) / THREADS; k++) {
         const int e = tid + THREADS * k;
@@ -909,23 +915,80 @@ __device__ __forceinline__ void finish_rows(const QmmArgs &a, const float *lds, 
         const int c4 = e & 7;
         const int row = m0 + 32 * t + r;
         const int col = colb + slot * 32 + 4 * c4;
-        if (row >= a.M || col >= a.N) continue;
+        const bool ok = row < a.M && col < a.N;
         const float4 s4 = *(const float4 *)(lds + ((slot * MT + t) * 32 + r) * kRowStride + 4 * c4);
         if (partial) {
-            *(float4 *)(a.partial + ((int64_t)sp * a.M + row) * a.N + col) = s4;
+            if (ok) *(float4 *)(a.partial + ((int64_t)sp * a.M + row) * a.N + col) = s4;
             continue;
         }
         const int64_t idx = (int64_t)row * a.N + col;
         const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
         float v[4], rv[4];
-        if (a.epi == VX_EPI_RESIDUAL) load4_dt(a.resid, idx, rv, a.y_dt);
+        if (ok && a.epi == VX_EPI_RESIDUAL) load4_dt(a.resid, idx, rv, a.y_dt);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             v[q] = round_dt(sv[q] * a.acc_scale, a.round_dt);
             if (a.epi == VX_EPI_RESIDUAL) v[q] = round_dt(rv[q] + v[q], a.round_dt);
             v[q] *= a.store_scale;
         }
-        store4_dt(a.y, idx, v, a.y_dt);
+        if (ok) store4_dt(a.y, idx, v, a.y_dt);
+        if (amax) {
+            // argmax over the stored values of the 32-column tile: the eight
+            // lanes of a row piece are lanes e % 8 of one wave (THREADS and
+            // the piece stride are multiples of 64); the tile winners meet in
+            // LDS past the row-major tiles
+            float bv = -__builtin_inff();
+            uint32_t bi = 0xffffffffu;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float x = round_dt(v[q], a.y_dt);
+                if (ok && x > bv) {  // strict: the first index wins ties; NaN never wins
+                    bv = x;
+                    bi = (uint32_t)(col + q);
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const uint32_t oi = (uint32_t)__shfl_xor((int)bi, o);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if (c4 == 0) {
+                float *wv = (float *)lds + 4 * MT * 32 * kRowStride;
+                uint32_t *wi = (uint32_t *)(wv + 4 * MT * 32);
+                wv[slot * MT * 32 + t * 32 + r] = bv;
+                wi[slot * MT * 32 + t * 32 + r] = bi;
+            }
+        }
+    }
+    if (amax) {
+        // one (value, first index) per row and workgroup (128 columns), at
+        // [row * ceil(N/128) + column block]; slots combine in column order
+        __syncthreads();
+        const float *wv = lds + 4 * MT * 32 * kRowStride;
+        const uint32_t *wi = (const uint32_t *)(wv + 4 * MT * 32);
+        for (int rl = tid; rl < MT * 32; rl += THREADS) {
+            const int row = m0 + rl;
+            if (row >= a.M) continue;
+            float bv = -__builtin_inff();
+            uint32_t bi = 0xffffffffu;
+#pragma unroll
+            for (int slot = 0; slot < 4; slot++) {
+                if (colb + slot * 32 >= a.N) break;
+                const float ov = wv[slot * MT * 32 + rl];
+                const uint32_t oi = wi[slot * MT * 32 + rl];
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            const int64_t at = (int64_t)row * ((a.N + 127) / 128) + colb / 128;
+            a.amax_v[at] = bv;
+            a.amax_i[at] = bi;
+        }
     }
 }
 
@@ -1141,7 +1204,7 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     // the clamped prefetches past the last step still write LDS: drain them
     // before the workgroup's LDS can be handed to another workgroup
     vm_wait<0>();
-    if constexpr (NT == 1 && R * BUF * 16 >= 4 * MT * 32 * kRowStride * 4) {
+    if constexpr (NT == 1 && R * BUF * 16 >= 4 * MT * 32 * kRowStride * 4 + 4 * MT * 32 * 8) {
         __syncthreads();
         acc_to_rows<MT>(acc, (float *)xs + wave * MT * 32 * kRowStride, lane, false);
         __syncthreads();
@@ -1173,7 +1236,7 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     static_assert(VM < 64, "vmcnt range");
     constexpr int XSLOTS = R * BUF;
     constexpr int CSLOTS = 4 * MT * NT * 16 * 64 / 4;  // float4 slots of the pair combine
-    constexpr int RSLOTS = 4 * MT * 32 * kRowStride / 4;  // ... of the row-major partial tiles
+    constexpr int RSLOTS = 4 * MT * 32 * kRowStride / 4 + 4 * MT * 32 * 8 / 16;  // ... row-major tiles + argmax
     constexpr int ESLOTS = CSLOTS > RSLOTS ? CSLOTS : RSLOTS;
     __shared__ __align__(256) uint4 xs[XSLOTS > ESLOTS ? XSLOTS : ESLOTS];
 
@@ -1695,7 +1758,7 @@ size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi, bool packed
 int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, void *y,
                const void *resid, int64_t M, int64_t N, int64_t K, int x_dt, int x_shift,
                int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
-               hipStream_t st, bool packed = false) {
+               hipStream_t st, bool packed = false, float *amax_v = nullptr, uint32_t *amax_i = nullptr) {
     Plan p = packed ? make_plan_p32(M, N, K, epi) : make_plan(M, N, K, epi, x_dt == VX_F16);
     if (epi == VX_EPI_SWIGLU && (N % 32 != 0 || (!p.p32 && p.NT % 2 != 0)))
         return set_error("qmm swiglu: N must be a multiple of 32 with paired tiles");
@@ -1707,7 +1770,9 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
             return set_error("qmm: workspace too small (see vx_qmm_workspace_size)");
         }
     }
-    QmmArgs a;
+    QmmArgs a{};
+    a.amax_v = amax_v;
+    a.amax_i = amax_i;
     a.x = x;
     a.w = w;
     a.s = (const uint16_t *)s;
@@ -1768,6 +1833,26 @@ int qmm_packed(const void *x, const void *packed, void *y, const void *resid, in
     if (((uintptr_t)x % 16) != 0 || ((uintptr_t)packed % 16) != 0) return set_error("qmm packed: misaligned operand");
     return qmm_launch(x, (const uint32_t *)packed, nullptr, nullptr, y, resid, M, N, K, VX_F16, x_shift, y_shift,
                       round_dt, y_dt, epi, workspace, ws_bytes, st, true);
+}
+
+// The packed STORE GEMM with greedy-argmax partials of its stored values
+// ((value, first index) per row and 128-column block, [M, N/128]): available
+// when the plan runs one split on a one-tile-per-wave kernel with the
+// row-major epilogue (qmm_packed_argmax_ok).
+bool qmm_packed_argmax_ok(int64_t M, int64_t N, int64_t K) {
+    if (N % 128 != 0 || K % 128 != 0) return false;
+    const Plan p = make_plan_p32(M, N, K, VX_EPI_STORE);
+    // the four-wave kernel holds the row-major tiles in its LDS ring from P = 2 on
+    const bool dma_rows = env_int("VX_QMM_DMA", 1) != 0 && env_int("VX_QMM_P", p.MT == 3 ? 2 : 3) >= 2;
+    return p.splits == 1 && p.NT == 1 && (p.k2 || dma_rows);
+}
+
+int qmm_packed_argmax(const void *x, const void *packed, void *y, int64_t M, int64_t N, int64_t K, int round_dt,
+                      int y_dt, float *amax_v, uint32_t *amax_i, void *workspace, size_t ws_bytes, hipStream_t st) {
+    if (!qmm_packed_argmax_ok(M, N, K)) return set_error("qmm packed argmax: the plan has no row-major epilogue");
+    if (((uintptr_t)x % 16) != 0 || ((uintptr_t)packed % 16) != 0) return set_error("qmm packed: misaligned operand");
+    return qmm_launch(x, (const uint32_t *)packed, nullptr, nullptr, y, nullptr, M, N, K, VX_F16, 0, 0, round_dt,
+                      y_dt, VX_EPI_STORE, workspace, ws_bytes, st, true, amax_v, amax_i);
 }
 
 // Packed GEMM whose epilogue writes raw f32 split partials into the
