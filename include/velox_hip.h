@@ -221,7 +221,6 @@ int vx_model_create(const vx_qwen3_config *cfg, const vx_weights_host *w, int64_
                     vx_model **out);
 void vx_model_destroy(vx_model *m);
 
-/* SeqSlice (qwen3.rs:254-263): block_table is a host array. */
 /* Tree-path KV compaction.  No counterpart in the reference (its spec loop
  * is a chain); tree verification (vx_forward with tree_parents) writes node j
  * of each sequence at position kv_offset + j, and after vx_accept_tree the
@@ -236,6 +235,7 @@ int vx_kv_compact_path(vx_pages *pages, const uint32_t *block_tables, int64_t ma
                        const uint32_t *kv_offsets, const int32_t *accepted, const int32_t *path,
                        int64_t n_seqs, int64_t r, void *stream);
 
+/* SeqSlice (qwen3.rs:254-263): block_table is a host array. */
 typedef struct {
     int64_t new_tokens, kv_offset;
     const uint32_t *block_table;
