@@ -306,6 +306,130 @@ int vx_spec_last_profile(const vx_spec *e, vx_step_profile *out);
 /* SpecEngine::free (spec.rs:320-323). */
 void vx_spec_free(vx_spec *e, int64_t state);
 
+/* Continuous batching support (the reference's scheduler admits a request,
+ * scheduler.rs:221-296, then prefills it inside its packed step, :299-368).
+ *
+ * vx_spec_add_state creates a state for prompt[0, len) without running
+ * anything.  Its first cached_tokens positions (a multiple of page_size,
+ * at most len - 1) are already in KV, in target_pages / draft_pages
+ * [cached_tokens / page_size]; the state takes over one reference to each
+ * (vx_spec_free releases it).  Pages covering max(reserve_tokens, len - 1)
+ * positions are allocated now, all or nothing over both pools ("not enough
+ * free pages" leaves everything as it was).  stream_id keys the state's
+ * Philox uniforms (rounds count from 0); temperature < 0 takes the engine's.
+ * The state is ready for vx_spec_step once prompt[..len-1] is in KV: at
+ * once when cached_tokens == len - 1, else after vx_spec_prefill_chunk has
+ * fed the rest.  Freed state numbers are reused. */
+int vx_spec_add_state(vx_spec *e, const uint32_t *prompt, int64_t len, int64_t cached_tokens,
+                      const uint32_t *target_pages, const uint32_t *draft_pages, int64_t reserve_tokens,
+                      uint32_t stream_id, float temperature, int64_t *out_state);
+/* One batched forward of both models over the next n_tokens[b] prompt
+ * tokens of each listed state (at positions kv_len .. kv_len + n_tokens - 1,
+ * never past len - 2); logits are discarded as in spec.rs:172-173. */
+int vx_spec_prefill_chunk(vx_spec *e, const int64_t *state_ids, const int64_t *n_tokens, int64_t n,
+                          void *stream);
+/* Block table of a state (which: 0 target, 1 draft); returns its length and
+ * copies up to cap entries; -1 for an unknown state. */
+int64_t vx_spec_state_pages(const vx_spec *e, int64_t state, int which, uint32_t *out, int64_t cap);
+
+/* ------------------------------------------------------------------------
+ * Continuous-batching speculative scheduler: BatchScheduler
+ * (scheduler.rs:37-534) with spec rounds in place of its one-token decode,
+ * and PrefixCache (prefix_cache.rs:1-230) over target + draft page pairs.
+ *
+ * Each vx_sched_step:
+ *  1. admits waiting requests in FCFS order while fewer than
+ *     max_running_requests run: a prefix-cache lookup (whole pages of
+ *     prompt[..len-1]), then vx_spec_add_state reserving len + max_new +
+ *     draft_k positions; a request that does not fit stays at the head of
+ *     the queue (scheduler.rs:221-296).  A request whose next uncached
+ *     prompt page another running request is still prefilling waits, so it
+ *     shares that page instead of computing it again.
+ *  2. walks the running requests by id under max_batch_tokens
+ *     (scheduler.rs:299-337): a prefilling request takes the rest of its
+ *     prompt, cut to the budget left (a chunk); a decoding request costs
+ *     draft_k + 1 verify rows and is deferred when they do not fit.  The
+ *     first request always runs.
+ *  3. runs one vx_spec_prefill_chunk for the chunks, registers every prompt
+ *     page completed by it in the prefix cache, and runs vx_spec_step for
+ *     the decoding requests (one call per distinct temperature).
+ *  4. appends committed tokens, stops at an EOS id ("stop") or max_new
+ *     tokens ("length"), truncating the round's surplus, and frees the
+ *     finished requests' states (scheduler.rs:369-500).
+ * ---------------------------------------------------------------------- */
+typedef struct vx_sched vx_sched;
+
+typedef struct {
+    int64_t max_running_requests;   /* scheduler.rs:37-59 default 64 */
+    int64_t max_batch_tokens;       /* default 512 */
+    int64_t prefix_cache_capacity;  /* cached page pairs; 0 disables; default 256 */
+    int64_t draft_k;                /* draft tokens per round */
+} vx_sched_config;
+
+/* SchedulerStats (scheduler.rs:94-105) plus the spec counters. */
+typedef struct {
+    uint64_t steps, tokens_generated, requests_completed, requests_aborted;
+    uint64_t last_batch_size, last_step_us;
+    uint64_t prefix_cache_hits, prefix_cache_misses, prefix_tokens_skipped;
+    uint64_t rounds, draft_tokens_accepted, prefill_tokens;
+} vx_sched_stats;
+
+/* The engine the scheduler drives.  vx_sched_create binds it to a vx_spec
+ * and its two page pools; vx_sched_create_with_backend takes any engine
+ * with these semantics (which: 0 target pool, 1 draft pool):
+ *  add_state / prefill_chunk / step / state_pages / free_state as the
+ *  vx_spec_* calls above (step with eos -1, on the scheduler's stream);
+ *  incref / decref as vx_pages_incref / vx_pages_free on a pool. */
+typedef struct {
+    void *ctx;
+    int64_t page_size;
+    int (*add_state)(void *ctx, const uint32_t *prompt, int64_t len, int64_t cached_tokens,
+                     const uint32_t *target_pages, const uint32_t *draft_pages, int64_t reserve_tokens,
+                     uint32_t stream_id, float temperature, int64_t *out_state);
+    int (*prefill_chunk)(void *ctx, const int64_t *states, const int64_t *n_tokens, int64_t n);
+    int (*step)(void *ctx, const int64_t *states, int64_t n, int64_t draft_k, vx_round_outcome *outcomes,
+                uint32_t *committed);
+    int64_t (*state_pages)(void *ctx, int64_t state, int which, uint32_t *out, int64_t cap);
+    void (*free_state)(void *ctx, int64_t state);
+    void (*incref)(void *ctx, int which, const uint32_t *pages, int64_t n);
+    void (*decref)(void *ctx, int which, const uint32_t *pages, int64_t n);
+} vx_sched_backend;
+
+/* BatchScheduler::new (scheduler.rs:108-137).  eos_ids: host array (the
+ * reference's eos_token_ids).  The engine must outlive the scheduler. */
+int vx_sched_create(vx_spec *engine, const vx_sched_config *cfg, const uint32_t *eos_ids, int64_t n_eos,
+                    void *stream, vx_sched **out);
+int vx_sched_create_with_backend(const vx_sched_backend *backend, const vx_sched_config *cfg,
+                                 const uint32_t *eos_ids, int64_t n_eos, vx_sched **out);
+/* Frees every live state and clears the prefix cache (PrefixCache::clear). */
+void vx_sched_destroy(vx_sched *s);
+/* BatchScheduler::submit (scheduler.rs:147-185) for a tokenised prompt:
+ * "Empty prompt" for len 0; a spec round needs len >= 2.  max_new_tokens
+ * is raised to 1 as in the reference.  temperature <= 1e-7 is greedy
+ * (scheduler.rs:555-559).  stream < 0 keys the Philox uniforms by the
+ * request id, so a request's samples do not depend on its batch mates.
+ * Returns ids 1, 2, 3, ... (RequestId, request.rs:11-21). */
+int vx_sched_submit(vx_sched *s, const uint32_t *prompt, int64_t len, int64_t max_new_tokens, float temperature,
+                    int64_t stream, int64_t *out_id);
+/* One scheduler step (admit + BatchScheduler::step); *out_tokens = the new
+ * tokens it fed to the models (0 when idle). */
+int vx_sched_step(vx_sched *s, int64_t *out_tokens);
+/* Request state: tokens generated so far (up to cap copied), status
+ * 0 waiting / 1 running / 2 finished / 3 aborted, finish reason 0 none /
+ * 1 stop / 2 length / 3 cancelled. */
+int vx_sched_poll(vx_sched *s, int64_t id, uint32_t *tokens, int64_t cap, int64_t *n_tokens, int *status,
+                  int *finish_reason);
+/* Cancel a waiting or running request (the reference's client disconnect,
+ * scheduler.rs:441-453); its pages go back at once. */
+int vx_sched_abort(vx_sched *s, int64_t id);
+/* Forget a finished or aborted request's record. */
+int vx_sched_release(vx_sched *s, int64_t id);
+int vx_sched_get_stats(vx_sched *s, vx_sched_stats *out);
+/* Requests waiting / running; page pairs held by the prefix cache. */
+int64_t vx_sched_num_waiting(vx_sched *s);
+int64_t vx_sched_num_running(vx_sched *s);
+int64_t vx_sched_cache_pages(vx_sched *s);
+
 #ifdef __cplusplus
 }
 #endif

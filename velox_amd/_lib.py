@@ -84,6 +84,33 @@ class StepProfile(C.Structure):
                 ("draft_kernel_bytes", C.c_double * 3), ("draft_kernel_launches", C.c_int64 * 3)]
 
 
+class SchedConfig(C.Structure):
+    _fields_ = [("max_running_requests", i64), ("max_batch_tokens", i64), ("prefix_cache_capacity", i64),
+                ("draft_k", i64)]
+
+
+class SchedStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "steps", "tokens_generated", "requests_completed", "requests_aborted", "last_batch_size", "last_step_us",
+        "prefix_cache_hits", "prefix_cache_misses", "prefix_tokens_skipped", "rounds", "draft_tokens_accepted",
+        "prefill_tokens")]
+
+
+i64p = C.POINTER(i64)
+ADD_STATE_FN = C.CFUNCTYPE(i32, vp, u32p, i64, i64, u32p, u32p, i64, C.c_uint32, f32, i64p)
+PREFILL_CHUNK_FN = C.CFUNCTYPE(i32, vp, i64p, i64p, i64)
+STEP_FN = C.CFUNCTYPE(i32, vp, i64p, i64, i64, C.POINTER(RoundOutcome), u32p)
+STATE_PAGES_FN = C.CFUNCTYPE(i64, vp, i64, i32, u32p, i64)
+FREE_STATE_FN = C.CFUNCTYPE(None, vp, i64)
+REF_FN = C.CFUNCTYPE(None, vp, i32, u32p, i64)
+
+
+class SchedBackend(C.Structure):
+    _fields_ = [("ctx", vp), ("page_size", i64), ("add_state", ADD_STATE_FN), ("prefill_chunk", PREFILL_CHUNK_FN),
+                ("step", STEP_FN), ("state_pages", STATE_PAGES_FN), ("free_state", FREE_STATE_FN),
+                ("incref", REF_FN), ("decref", REF_FN)]
+
+
 _SIGS = {
     "vx_last_error": (C.c_char_p, []),
     "vx_version": (C.c_char_p, []),
@@ -129,6 +156,22 @@ _SIGS = {
     "vx_spec_free": (None, [vp, i64]),
     "vx_spec_set_profiling": (i32, [vp, i32]),
     "vx_spec_last_profile": (i32, [vp, C.POINTER(StepProfile)]),
+    "vx_spec_add_state": (i32, [vp, u32p, i64, i64, u32p, u32p, i64, C.c_uint32, f32, C.POINTER(i64)]),
+    "vx_spec_prefill_chunk": (i32, [vp, C.POINTER(i64), C.POINTER(i64), i64, vp]),
+    "vx_spec_state_pages": (i64, [vp, i64, i32, u32p, i64]),
+    "vx_sched_create": (i32, [vp, C.POINTER(SchedConfig), u32p, i64, vp, C.POINTER(vp)]),
+    "vx_sched_create_with_backend": (i32, [C.POINTER(SchedBackend), C.POINTER(SchedConfig), u32p, i64,
+                                           C.POINTER(vp)]),
+    "vx_sched_destroy": (None, [vp]),
+    "vx_sched_submit": (i32, [vp, u32p, i64, i64, f32, i64, C.POINTER(i64)]),
+    "vx_sched_step": (i32, [vp, C.POINTER(i64)]),
+    "vx_sched_poll": (i32, [vp, i64, u32p, i64, C.POINTER(i64), C.POINTER(i32), C.POINTER(i32)]),
+    "vx_sched_abort": (i32, [vp, i64]),
+    "vx_sched_release": (i32, [vp, i64]),
+    "vx_sched_get_stats": (i32, [vp, C.POINTER(SchedStats)]),
+    "vx_sched_num_waiting": (i64, [vp]),
+    "vx_sched_num_running": (i64, [vp]),
+    "vx_sched_cache_pages": (i64, [vp]),
 }
 
 for _name, (_res, _args) in _SIGS.items():

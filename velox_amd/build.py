@@ -1,8 +1,9 @@
 """Build libvelox_hip.so (gfx950) in-tree with hipcc.
 
-Every translation unit is compiled in parallel, then linked into
-velox_amd/libvelox_hip.so.  Packed-FP32 instruction selection is disabled
-(`-packed-fp32-ops`) for all device code.
+Every translation unit is compiled in parallel (the .hip files by hipcc,
+the host-only .cpp files by g++), then linked into velox_amd/libvelox_hip.so.
+Packed-FP32 instruction selection is disabled (`-packed-fp32-ops`) for all
+device code.
 """
 from __future__ import annotations
 
@@ -17,7 +18,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libvelox_hip.so")
-SOURCES = ["qmm.hip", "attn.hip", "ops.hip", "engine.hip"]
+SOURCES = ["qmm.hip", "attn.hip", "ops.hip", "engine.hip", "sched.cpp"]
 ARCH = os.environ.get("VX_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -35,12 +36,18 @@ def hipcc() -> str:
     return path
 
 
+HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-I", os.path.join(ROOT, "include"), "-Wall"]
+
+
 def _compile(src: str) -> str:
     out = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", os.path.join(CSRC, src), "-o", out]
+    if src.endswith(".cpp"):  # host-only code: no device pass
+        cmd = [shutil.which("g++") or "g++", *HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", out]
+    else:
+        cmd = [hipcc(), *FLAGS, "-c", os.path.join(CSRC, src), "-o", out]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-6000:]}")
+        raise RuntimeError(f"compile failed for {src}:\n{r.stderr[-6000:]}")
     return out
 
 

@@ -913,7 +913,10 @@ struct SpecState {
     uint32_t last_token = 0;
     std::vector<uint32_t> tokens;
     uint32_t stream_id = 0, round = 0;
+    float temperature = 0.f;
+    int64_t prompt_len = 0;  // tokens[0, prompt_len) is the prompt
     bool live = false;
+    bool ready = false;      // prompt[..len-1] is in both caches: rounds may run
 };
 }  // namespace
 
@@ -927,6 +930,7 @@ struct vx_spec {
     // device buffers for a round
     DevBuf d_ids, d_cand, d_vids, d_tlog, d_dlog, d_acc, d_tok, d_uni, d_meta, d_argws, d_draw;
     DevBuf d_amax;  // greedy-argmax partials written by the LM heads: values then indices
+    DevBuf d_plog;  // prefill-chunk logits (discarded, spec.rs:172-173)
     // host staging (pinned)
     void *h_stage = nullptr;
     size_t h_stage_n = 0;
@@ -1023,7 +1027,10 @@ extern "C" int vx_spec_prefill(vx_spec *e, const uint32_t *const *prompts, const
         s.kv_len = head;
         s.last_token = prompts[b][head];
         s.tokens.assign(prompts[b], prompts[b] + lens[b]);
+        s.prompt_len = lens[b];
+        s.temperature = e->temperature;
         s.live = true;
+        s.ready = true;
         e->states.push_back(std::move(s));
         ids.insert(ids.end(), prompts[b], prompts[b] + head);
     }
@@ -1042,6 +1049,101 @@ extern "C" int vx_spec_prefill(vx_spec *e, const uint32_t *const *prompts, const
     if (vx_forward(e->draft, e->dp, ids.data(), sl.data(), n, 0, nullptr, lg.p, nullptr)) return rollback();
     *out_first_state = first;
     return 0;
+}
+
+extern "C" int vx_spec_add_state(vx_spec *e, const uint32_t *prompt, int64_t len, int64_t cached_tokens,
+                                 const uint32_t *target_pages, const uint32_t *draft_pages, int64_t reserve_tokens,
+                                 uint32_t stream_id, float temperature, int64_t *out_state) {
+    VX_REQUIRE(e && prompt && out_state, "add_state: null argument");
+    int64_t ps;
+    VX_TRY(page_size_or_err(e, &ps));
+    VX_REQUIRE(len >= 2, "speculative prefill requires a prompt with at least 2 tokens");
+    VX_REQUIRE(cached_tokens >= 0 && cached_tokens <= len - 1 && cached_tokens % ps == 0,
+               "add_state: cached_tokens must be a multiple of page_size and at most len - 1");
+    VX_REQUIRE(cached_tokens == 0 || (target_pages && draft_pages), "add_state: cached pages missing");
+    SpecState s;
+    const int64_t nc = cached_tokens / ps;
+    s.target_blocks.assign(target_pages, target_pages + nc);
+    s.draft_blocks.assign(draft_pages, draft_pages + nc);
+    const int64_t need = (std::max(reserve_tokens, len - 1) + ps - 1) / ps;
+    // all-or-nothing over both pools: the caller's cached references stay its own on failure
+    if (need - nc > vx_pages_num_free(e->tp) || need - nc > vx_pages_num_free(e->dp))
+        return set_error("add_state: not enough free pages");
+    {
+        std::vector<uint32_t> t = s.target_blocks, d = s.draft_blocks;
+        VX_TRY(ensure_capacity(e->tp, t, need, "alloc target pages"));
+        if (ensure_capacity(e->dp, d, need, "alloc draft pages")) {
+            vx_pages_free(e->tp, t.data() + nc, (int64_t)t.size() - nc);
+            return -1;
+        }
+        s.target_blocks.swap(t);
+        s.draft_blocks.swap(d);
+    }
+    s.kv_len = cached_tokens;
+    s.tokens.assign(prompt, prompt + len);
+    s.prompt_len = len;
+    s.stream_id = stream_id;
+    s.temperature = temperature < 0.f ? e->temperature : temperature;
+    s.live = true;
+    s.ready = cached_tokens == len - 1;
+    if (s.ready) s.last_token = prompt[len - 1];
+    int64_t slot = 0;
+    while (slot < (int64_t)e->states.size() && e->states[slot].live) slot++;
+    if (slot == (int64_t)e->states.size()) e->states.emplace_back();
+    e->states[slot] = std::move(s);
+    *out_state = slot;
+    return 0;
+}
+
+extern "C" int vx_spec_prefill_chunk(vx_spec *e, const int64_t *state_ids, const int64_t *n_tokens, int64_t n,
+                                     void *stream) {
+    VX_REQUIRE(e && (n == 0 || (state_ids && n_tokens)), "prefill_chunk: null argument");
+    int64_t ps;
+    VX_TRY(page_size_or_err(e, &ps));
+    if (n == 0) return 0;
+    std::vector<SpecState *> S(n);
+    std::vector<uint32_t> ids;
+    for (int64_t b = 0; b < n; b++) {
+        VX_REQUIRE(state_ids[b] >= 0 && state_ids[b] < (int64_t)e->states.size() && e->states[state_ids[b]].live,
+                   "prefill_chunk: unknown state");
+        SpecState &s = e->states[state_ids[b]];
+        VX_REQUIRE(!s.ready, "prefill_chunk: state has no prompt left to prefill");
+        VX_REQUIRE(n_tokens[b] >= 1 && s.kv_len + n_tokens[b] <= s.prompt_len - 1,
+                   "prefill_chunk: chunk runs past prompt[..len-1]");
+        for (int64_t c = 0; c < b; c++)
+            VX_REQUIRE(state_ids[c] != state_ids[b], "prefill_chunk: state listed twice");
+        S[b] = &s;
+    }
+    for (int64_t b = 0; b < n; b++) {
+        const int64_t end = S[b]->kv_len + n_tokens[b];
+        VX_TRY(ensure_capacity(e->tp, S[b]->target_blocks, (end + ps - 1) / ps, "alloc target prefill pages"));
+        VX_TRY(ensure_capacity(e->dp, S[b]->draft_blocks, (end + ps - 1) / ps, "alloc draft prefill pages"));
+        ids.insert(ids.end(), S[b]->tokens.begin() + S[b]->kv_len, S[b]->tokens.begin() + end);
+    }
+    VX_TRY(e->d_plog.ensure((size_t)n * e->target->cfg.vocab * 2));
+    std::vector<vx_seq_slice> sl(n);
+    for (int64_t b = 0; b < n; b++)
+        sl[b] = {n_tokens[b], S[b]->kv_len, S[b]->target_blocks.data(), (int64_t)S[b]->target_blocks.size()};
+    VX_TRY(vx_forward(e->target, e->tp, ids.data(), sl.data(), n, 0, nullptr, e->d_plog.p, stream));
+    for (int64_t b = 0; b < n; b++)
+        sl[b] = {n_tokens[b], S[b]->kv_len, S[b]->draft_blocks.data(), (int64_t)S[b]->draft_blocks.size()};
+    VX_TRY(vx_forward(e->draft, e->dp, ids.data(), sl.data(), n, 0, nullptr, e->d_plog.p, stream));
+    for (int64_t b = 0; b < n; b++) {
+        SpecState &s = *S[b];
+        s.kv_len += n_tokens[b];
+        if (s.kv_len == s.prompt_len - 1) {
+            s.ready = true;
+            s.last_token = s.tokens[s.prompt_len - 1];
+        }
+    }
+    return 0;
+}
+
+extern "C" int64_t vx_spec_state_pages(const vx_spec *e, int64_t s, int which, uint32_t *out, int64_t cap) {
+    if (!e || s < 0 || s >= (int64_t)e->states.size() || !e->states[s].live) return -1;
+    const auto &bt = which ? e->states[s].draft_blocks : e->states[s].target_blocks;
+    if (out) memcpy(out, bt.data(), (size_t)std::min<int64_t>(cap, (int64_t)bt.size()) * 4);
+    return (int64_t)bt.size();
 }
 
 namespace {
@@ -1076,7 +1178,10 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
         VX_REQUIRE(state_ids[b] >= 0 && state_ids[b] < (int64_t)e->states.size() && e->states[state_ids[b]].live,
                    "step: unknown state");
         S[b] = &e->states[state_ids[b]];
+        VX_REQUIRE(S[b]->ready, "step: state is still prefilling");
+        VX_REQUIRE(S[b]->temperature == S[0]->temperature, "step: states of one round must share a temperature");
     }
+    const float temp = n > 0 ? S[0]->temperature : e->temperature;
     // capacity (spec.rs:198-205)
     for (int64_t b = 0; b < n; b++) {
         VX_TRY(ensure_capacity(e->tp, S[b]->target_blocks, (S[b]->kv_len + D + 1 + ps - 1) / ps, "grow target block table"));
@@ -1121,7 +1226,7 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     VX_TRY(e->d_cand.ensure(n * D * 4));
     VX_TRY(e->d_vids.ensure(n * (D + 1) * 4));
     VX_TRY(e->d_tlog.ensure((size_t)n * (D + 1) * V * 2));
-    const bool stoch = e->temperature > 0.f;
+    const bool stoch = temp > 0.f;
     VX_TRY(e->d_dlog.ensure((size_t)n * (stoch ? D : 1) * V * 2));
     VX_TRY(e->d_acc.ensure(n * 4));
     VX_TRY(e->d_tok.ensure(n * (D + 1) * 4));
@@ -1180,7 +1285,7 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
                                         nullptr, cand + i, D, e->d_argws.p, e->d_argws.n, st));
         } else {
             VX_TRY(sample_rows_launch(dl, VX_BF16, uni + i * 4, (D + 1) * 4, (uint32_t *)e->d_draw.p, n, V,
-                                      e->temperature, cand + i, D, e->d_argws.p, e->d_argws.n, st));
+                                      temp, cand + i, D, e->d_argws.p, e->d_argws.n, st));
         }
         if (i + 1 < D)  // next draft input = column i of cand [n, D]
             VX_HIP(hipMemcpy2DAsync(ids, 4, cand + i, D * 4, 4, n, hipMemcpyDeviceToDevice, st));
@@ -1212,7 +1317,7 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
             VX_HIP(hipMemcpy2DAsync((uint16_t *)tmp.p + i * V, D * V * 2, (uint16_t *)e->d_dlog.p + (size_t)i * n * V,
                                     V * 2, V * 2, n, hipMemcpyDeviceToDevice, st));
         VX_TRY(stochastic_accept_launch(e->d_tlog.p, tmp.p, VX_BF16, cand, uni, (int32_t *)e->d_acc.p,
-                                        (uint32_t *)e->d_tok.p, n, D, V, e->temperature, e->d_argws.p, e->d_argws.n,
+                                        (uint32_t *)e->d_tok.p, n, D, V, temp, e->d_argws.p, e->d_argws.n,
                                         st));
         VX_HIP(hipStreamSynchronize(st));
     }
@@ -1330,3 +1435,57 @@ extern "C" void vx_spec_free(vx_spec *e, int64_t s) {
 
 extern "C" const char *vx_last_error(void) { return g_err.c_str(); }
 extern "C" const char *vx_version(void) { return "velox_amd 0.1.0 (gfx950)"; }
+
+// ===========================================================================
+// the scheduler's engine binding (vx_sched_create)
+// ===========================================================================
+namespace {
+struct SpecBinding {
+    vx_spec *e;
+    void *stream;
+};
+int sb_add_state(void *c, const uint32_t *prompt, int64_t len, int64_t cached, const uint32_t *tp,
+                 const uint32_t *dp, int64_t reserve, uint32_t stream_id, float temperature, int64_t *out) {
+    return vx_spec_add_state(((SpecBinding *)c)->e, prompt, len, cached, tp, dp, reserve, stream_id, temperature, out);
+}
+int sb_prefill_chunk(void *c, const int64_t *states, const int64_t *n_tokens, int64_t n) {
+    auto *b = (SpecBinding *)c;
+    return vx_spec_prefill_chunk(b->e, states, n_tokens, n, b->stream);
+}
+int sb_step(void *c, const int64_t *states, int64_t n, int64_t k, vx_round_outcome *outcomes, uint32_t *committed) {
+    auto *b = (SpecBinding *)c;
+    return vx_spec_step(b->e, states, n, k, -1, outcomes, committed, b->stream);
+}
+int64_t sb_state_pages(void *c, int64_t s, int which, uint32_t *out, int64_t cap) {
+    return vx_spec_state_pages(((SpecBinding *)c)->e, s, which, out, cap);
+}
+void sb_free_state(void *c, int64_t s) { vx_spec_free(((SpecBinding *)c)->e, s); }
+void sb_incref(void *c, int which, const uint32_t *pages, int64_t n) {
+    vx_spec *e = ((SpecBinding *)c)->e;
+    vx_pages_incref(which ? e->dp : e->tp, pages, n);
+}
+void sb_decref(void *c, int which, const uint32_t *pages, int64_t n) {
+    vx_spec *e = ((SpecBinding *)c)->e;
+    vx_pages_free(which ? e->dp : e->tp, pages, n);
+}
+void sb_release(void *c) { delete (SpecBinding *)c; }
+}  // namespace
+
+namespace vx {
+int spec_sched_backend(vx_spec *e, void *stream, vx_sched_backend *out, void (**release)(void *)) {
+    int64_t ps;
+    VX_TRY(page_size_or_err(e, &ps));
+    *out = vx_sched_backend{};
+    out->ctx = new SpecBinding{e, stream};
+    out->page_size = ps;
+    out->add_state = sb_add_state;
+    out->prefill_chunk = sb_prefill_chunk;
+    out->step = sb_step;
+    out->state_pages = sb_state_pages;
+    out->free_state = sb_free_state;
+    out->incref = sb_incref;
+    out->decref = sb_decref;
+    *release = sb_release;
+    return 0;
+}
+}  // namespace vx
