@@ -16,6 +16,7 @@ one round of the same workload with a 4-token prompt.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
   python bench.py --mode qmm   # config 1: isolated verify GEMMs, cache-rotated
+  python bench.py --mode continuous   # config 4: scheduler, Qwen3-8B shape
 """
 from __future__ import annotations
 
@@ -244,6 +245,95 @@ def run_qmm(args):
     print(json.dumps({"mode": "qmm", "results": out}), flush=True)
 
 
+def run_continuous(args):
+    """Config 4: continuous-batching speculative decoding on a random-init
+    Qwen3-8B-shaped int4 g64 model: 32 requests, prompt lengths U[256, 4096]
+    whose first 512 tokens are shared within groups of 8, k = 6 from the
+    target's first 2 layers, temperature 0.7 (Philox streams per request,
+    seed 4), 256 new tokens each, 16-token pages, through the scheduler
+    (vx_sched_*) with its prefix cache.  value = generated tokens / wall time
+    from the first submit to the last finished request (prefill included);
+    also the decode-only rate over the steps that ran no prefill."""
+    import torch
+
+    from velox_amd import engine, synth
+    from velox_amd.scheduler import BatchScheduler, SchedulerConfig
+
+    torch.cuda.set_device(0)
+    n_req, k, new_tokens, group, shared_len = 32, 6, 256, 8, 512
+    cfg = synth.qwen3_config("qwen3-8b", max_pos=8192)
+    t0 = time.time()
+    w = synth.host_weights(cfg, seed=4)
+    log(f"[cont] synthetic Qwen3-8B weights generated in {time.time() - t0:.1f}s")
+    target = engine.PagedQwen3(cfg, w)
+    draft = engine.PagedQwen3(cfg, w, n_layers=2)
+    del w
+    log(f"[cont] models on device ({time.time() - t0:.1f}s)")
+    rng = np.random.Generator(np.random.Philox(key=[4, 0x636F6E74]))
+    lens = rng.integers(256, 4097, size=n_req)
+    V = cfg["vocab"]
+    shared = [synth.prompt(4, shared_len, V, stream=1000 + g) for g in range(n_req // group)]
+    # a prompt shorter than the shared prefix is a prefix of it
+    prompts = [np.concatenate([shared[i // group][:int(lens[i])],
+                               synth.prompt(4, max(0, int(lens[i]) - shared_len), V, stream=i)])
+               for i in range(n_req)]
+    ps = 16
+    pages = sum(-(-(int(n) + new_tokens + k + 1) // ps) for n in lens) + 64
+    HK, D = cfg["n_kv_heads"], cfg["head_dim"]
+    tp = engine.PagedKvCache(cfg["layers"], HK, D, ps, pages)
+    dp = engine.PagedKvCache(2, HK, D, ps, pages)
+    e = engine.SpecEngine(target, tp, draft, dp, temperature=0.7, sample_seed=4)
+    scfg = SchedulerConfig(max_running_requests=n_req, max_batch_tokens=args.batch_tokens,
+                           prefix_cache_capacity=1024, draft_k=k)
+    # warm-up: grow every device buffer to the sizes the run needs, on unrelated prompts
+    s = BatchScheduler(e, (), scfg)
+    for i in range(n_req):
+        s.submit(synth.prompt(5, args.batch_tokens // n_req + 2, V, stream=i), 8, temperature=0.7)
+    s.run()
+    s.close()
+    torch.cuda.synchronize()
+    log(f"[cont] warm-up done ({time.time() - t0:.1f}s); {pages} pages per pool")
+    s = BatchScheduler(e, (), scfg)
+    torch.cuda.synchronize()
+    ts = time.perf_counter()
+    ids = [s.submit(p, new_tokens, temperature=0.7) for p in prompts]
+    dec_s, dec_tok, steps, last_log = 0.0, 0, 0, ts
+    while s.num_waiting() + s.num_running():
+        before = s.stats()
+        a = time.perf_counter()
+        s.step()
+        b = time.perf_counter()
+        after = s.stats()
+        steps += 1
+        if after["prefill_tokens"] == before["prefill_tokens"]:
+            dec_s += b - a
+            dec_tok += after["tokens_generated"] - before["tokens_generated"]
+        if b - last_log > 20:
+            log(f"[cont] step {steps}: {after['tokens_generated']} tokens, {s.num_running()} running, "
+                f"{s.num_waiting()} waiting")
+            last_log = b
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - ts
+    st = s.stats()
+    gen = sum(len(s.poll(r).tokens) for r in ids)
+    assert gen == n_req * new_tokens, f"generated {gen} tokens, expected {n_req * new_tokens}"
+    res = {
+        "mode": "continuous", "metric": "generated tok/s, config 4 (Qwen3-8B shape int4, 32 requests, k=6, T=0.7)",
+        "value": gen / wall, "unit": "generated tok/s", "wall_s": wall, "steps": steps,
+        "decode_tok_s": dec_tok / dec_s if dec_s else None, "decode_s": dec_s,
+        "prefill_tokens": st["prefill_tokens"], "prefix_tokens_skipped": st["prefix_tokens_skipped"],
+        "prefix_cache_hits": st["prefix_cache_hits"], "rounds": st["rounds"],
+        "acceptance_rate": st["draft_tokens_accepted"] / max(1, st["draft_tokens_proposed"]),
+        "config": {"workload": "continuous-batching spec decode", "model": "Qwen3-8B shape int4 g64",
+                   "requests": n_req, "prompt_len": "U[256, 4096]", "shared_prefix": f"{shared_len} per {group}",
+                   "k": k, "draft_layers": 2, "temperature": 0.7, "new_tokens": new_tokens,
+                   "max_batch_tokens": args.batch_tokens},
+        "data": "synthetic (random-init weights, Philox prompts)",
+    }
+    s.close()
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,7 +343,8 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=128)
-    ap.add_argument("--mode", choices=["spec", "qmm"], default="spec")
+    ap.add_argument("--mode", choices=["spec", "qmm", "continuous"], default="spec")
+    ap.add_argument("--batch-tokens", type=int, default=8192, help="continuous mode: max_batch_tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
                     help="first do one device copy of MB MiB (counter calibration for rocprofv3 --pmc)")
@@ -264,6 +355,8 @@ def main():
         sys.exit(2)
     if args.mode == "qmm":
         run_qmm(args)
+    elif args.mode == "continuous":
+        run_continuous(args)
     else:
         run_spec(args)
 

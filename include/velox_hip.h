@@ -371,7 +371,7 @@ typedef struct {
     uint64_t steps, tokens_generated, requests_completed, requests_aborted;
     uint64_t last_batch_size, last_step_us;
     uint64_t prefix_cache_hits, prefix_cache_misses, prefix_tokens_skipped;
-    uint64_t rounds, draft_tokens_accepted, prefill_tokens;
+    uint64_t rounds, draft_tokens_proposed, draft_tokens_accepted, prefill_tokens;
 } vx_sched_stats;
 
 /* The engine the scheduler drives.  vx_sched_create binds it to a vx_spec

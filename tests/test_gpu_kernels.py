@@ -117,6 +117,30 @@ def test_qmm_config1_f16(cuda, m, shape, path):
     assert_allclose_elementwise(f"cfg1 m{m} {n}x{k}", got, vxo.round_to(cpu, vxo.F16), 1e-2, 1e-2)
 
 
+QWEN3_8B_SHAPES = [(6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288), (151936, 4096)]
+
+
+@pytest.mark.parametrize("m", [7, 32, 224, 600])
+@pytest.mark.parametrize("shape", QWEN3_8B_SHAPES, ids=lambda s: f"n{s[0]}k{s[1]}")
+def test_qmm_qwen3_8b_shapes(cuda, m, shape):
+    """Config 4's GEMMs (Qwen3-8B: qkv, o, gate|up, down, LM head) on the
+    packed path at the k = 6 verify row counts (7 per sequence, 224 for 32
+    sequences), the 32-row draft and a 600-row prefill chunk; columns sampled
+    for the oracle."""
+    from velox_amd import _lib
+
+    n, k = shape
+    lin = synth_linear(n, k, 2)
+    rng = np.random.Generator(np.random.Philox(key=[2, n * 7 + k + m]))
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    run_qmm("packed", dev(x), lin, n, y, round_dtype=_lib.F16)
+    cols = np.sort(np.random.default_rng(m).choice(n, 1024, replace=False))
+    cpu = vxo.qmm_4bit(x.astype(np.float32), lin["qweight"][cols], lin["scales"][cols].astype(np.float32),
+                       lin["biases"][cols].astype(np.float32), None, 64, threads=8)
+    assert_allclose_elementwise(f"8b m{m} {n}x{k}", host(y)[:, cols], vxo.round_to(cpu, vxo.F16), 1e-2, 1e-2)
+
+
 @pytest.mark.parametrize("m", [1, 5, 16, 80, 97])
 def test_qmm_bf16_fast_path_shapes(cuda, m):
     """bf16 activations (the reference's bf16 contract) through the MFMA path."""

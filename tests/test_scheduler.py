@@ -201,6 +201,8 @@ def test_generates_greedy_continuations_and_returns_pages():
     assert st["requests_completed"] == 3 and st["steps"] == steps
     assert st["tokens_generated"] == 36
     assert st["prefill_tokens"] == sum(len(p) - 1 for p in ps_)
+    assert st["draft_tokens_proposed"] == 4 * sum(len(a) for kind, a in eng.calls if kind == "step")
+    assert 0 < st["draft_tokens_accepted"] < st["draft_tokens_proposed"]
     assert eng.free_pages() == [64, 64] and not eng.errors
     # the stream of a request defaults to its id
     s.release(1)

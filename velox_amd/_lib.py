@@ -92,8 +92,8 @@ class SchedConfig(C.Structure):
 class SchedStats(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in (
         "steps", "tokens_generated", "requests_completed", "requests_aborted", "last_batch_size", "last_step_us",
-        "prefix_cache_hits", "prefix_cache_misses", "prefix_tokens_skipped", "rounds", "draft_tokens_accepted",
-        "prefill_tokens")]
+        "prefix_cache_hits", "prefix_cache_misses", "prefix_tokens_skipped", "rounds", "draft_tokens_proposed",
+        "draft_tokens_accepted", "prefill_tokens")]
 
 
 i64p = C.POINTER(i64)

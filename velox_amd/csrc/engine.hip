@@ -931,6 +931,7 @@ struct vx_spec {
     DevBuf d_ids, d_cand, d_vids, d_tlog, d_dlog, d_acc, d_tok, d_uni, d_meta, d_argws, d_draw;
     DevBuf d_amax;  // greedy-argmax partials written by the LM heads: values then indices
     DevBuf d_plog;  // prefill-chunk logits (discarded, spec.rs:172-173)
+    DevBuf d_dlog_t;  // stochastic rounds: draft logits as [n][D][V]
     // host staging (pinned)
     void *h_stage = nullptr;
     size_t h_stage_n = 0;
@@ -1310,16 +1311,14 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
                                     0, e->d_argws.p, e->d_argws.n, st));
     } else {
         // draft logits are laid out [D][n][V]; the acceptance expects [n][D][V]
-        DevBuf tmp;
+        DevBuf &tmp = e->d_dlog_t;
         VX_TRY(tmp.ensure((size_t)n * D * V * 2));
-        VX_HIP(hipMemcpy2DAsync(tmp.p, D * V * 2, e->d_dlog.p, V * 2, V * 2, n, hipMemcpyDeviceToDevice, st));
-        for (int64_t i = 1; i < D; i++)
+        for (int64_t i = 0; i < D; i++)
             VX_HIP(hipMemcpy2DAsync((uint16_t *)tmp.p + i * V, D * V * 2, (uint16_t *)e->d_dlog.p + (size_t)i * n * V,
                                     V * 2, V * 2, n, hipMemcpyDeviceToDevice, st));
         VX_TRY(stochastic_accept_launch(e->d_tlog.p, tmp.p, VX_BF16, cand, uni, (int32_t *)e->d_acc.p,
                                         (uint32_t *)e->d_tok.p, n, D, V, temp, e->d_argws.p, e->d_argws.n,
                                         st));
-        VX_HIP(hipStreamSynchronize(st));
     }
     // ---- results to host (one copy set, one sync)
     uint8_t *hr = hs + total + small;

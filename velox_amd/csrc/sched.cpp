@@ -391,6 +391,7 @@ struct vx_sched {
             stats.rounds++;
             for (int64_t b = 0; b < n; b++) {
                 Request &r = *grp[b];
+                stats.draft_tokens_proposed += (uint64_t)k;
                 stats.draft_tokens_accepted += (uint64_t)std::max(out[b].accepted, 0);
                 for (int32_t i = 0; i < out[b].n_committed; i++) {
                     const uint32_t t = com[(size_t)b * (k + 1) + i];
