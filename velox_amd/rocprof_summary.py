@@ -68,7 +68,7 @@ def _verify_ops(ds, rounds):
     ops = []
     prev_gate_up = False
     for n, s, e, gx, gy, d in ds:
-        m = re.match(r"qmm_f16_(?:dma|k2)_kernel<(\d+), (\d+), (\d+)>", n)
+        m = re.match(r"qmm_f16_(?:dma|k2)_kernel<(\d+), (\d+), (\d+)(?:, \d+)?>", n)
         if m and m.group(1) == "3" and gy == 1:
             ops.append([(n, s, e, d)])
             prev_gate_up = True
