@@ -129,6 +129,14 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     const int hk = item % a.h_kv;
     const int seq = item / a.h_kv;
 
+    // the block-table entry of the wave's first key block depends on neither
+    // the row metadata nor the key range: request it with the metadata, so
+    // the K/V requests follow one round trip after entry, not two.  The
+    // index is clamped to the table row and the page to the pool, so an
+    // entry past the sequence's keys is a harmless in-bounds read.
+    const uint32_t *btr = a.bt + (int64_t)seq * a.max_blocks;
+    uint32_t bt_next = btr[min((split * a.chunk + wave * kKeyBlock + lane) / a.ps, a.max_blocks - 1)];
+
     int r_seq, row0, off;
     row_info(a, seq, r_seq, row0, off);
     if (a.mode == 1 && (int)a.kvo[seq] == 0) r_seq = 0;  // kv_len 0: zero-filled by the launcher
@@ -283,16 +291,16 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
 
     const int64_t head_stride = (int64_t)a.ps * D;
     const int64_t page_stride = (int64_t)a.h_kv * head_stride;
-    const uint32_t *btr = a.bt + (int64_t)seq * a.max_blocks;
     const int win = (int)a.window;
 
     for (int kb = k_lo + wave * kKeyBlock; kb < k_hi; kb += kAttnWaves * kKeyBlock) {
         // ---- request K (4 tiles of 16 keys, lane = key within a tile) and V
-        // (lane = key) of the block together, so both round trips overlap
-        // lane l looks up the page of key kb + l once; the K rows take theirs
-        // by lane exchange, so one block-table round trip precedes both
+        // (lane = key) of the block together, so both round trips overlap.
+        // Lane l holds the page of key kb + l (requested one block ahead);
+        // the K rows take theirs by lane exchange.
         const int vkey = kb + lane;
-        const int vpage = min((int)btr[min(vkey / a.ps, a.max_blocks - 1)], a.num_pages - 1);
+        const int vpage = min((int)bt_next, a.num_pages - 1);
+        bt_next = btr[min((kb + kAttnWaves * kKeyBlock + lane) / a.ps, a.max_blocks - 1)];
         frag kf[4][DK];
 #pragma unroll
         for (int mt = 0; mt < 4; mt++) {
@@ -683,6 +691,8 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
     a.scale_log2 = scale * 1.44269504088896341f;
     a.window = window;
     if (total_q == 0 || n_seqs == 0) return 0;
+    // the kernels read the block table before they know the key range
+    if (max_blocks < 1 || num_pages < 1 || ps < 1) return set_error("paged_attention: empty pool or block table");
     if (dtype == VX_F32) {
         const int threads = 256;
         hipLaunchKernelGGL(paged_attn_ref_kernel<VX_F32>, dim3((unsigned)total_q, (unsigned)h_q), dim3(threads),
