@@ -288,6 +288,49 @@ def test_decode_attention_reference_cases(cuda, case):
     assert_close(f"decode {dt}", host(out), cpu, atol, rtol)
 
 
+def test_sliding_window_decode_reference_case(cuda):
+    """metal_swa_parity.rs:48-170: one bf16 decode row, kv_len 96, window 32
+    (visible positions 64..95): matches the oracle and differs from the
+    global result (the window is not silently ignored)."""
+    from velox_amd import ops
+
+    hq, hk, d, ps, mb, p, kv_len, window = 8, 4, 64, 16, 8, 8, 96, 32
+    scale = 1.0 / np.sqrt(d)
+    q = vxo.round_to(rand_vec(hq * d, 11), vxo.BF16).reshape(1, hq, d)
+    k = vxo.round_to(rand_vec(p * hk * ps * d, 12), vxo.BF16).reshape(p, hk, ps, d)
+    v = vxo.round_to(rand_vec(p * hk * ps * d, 13), vxo.BF16).reshape(p, hk, ps, d)
+    bt = np.arange(mb, dtype=np.uint32).reshape(1, mb)
+    args = (dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(v, torch.bfloat16), u32(bt),
+            u32(np.array([kv_len], np.uint32)), scale)
+    swa = host(ops.paged_decode_attention(*args, sliding_window=window))
+    glob = host(ops.paged_decode_attention(*args))
+    cpu = vxo.paged_attention(q, k, v, bt, np.array([0, 1], np.uint32), np.array([kv_len - 1], np.uint32), scale,
+                              sliding_window=window)
+    assert_close("decode swa", swa, cpu, 3e-2, 3e-2)
+    assert np.abs(glob - swa).max() > 1e-2, "the window did not change the output"
+
+
+def test_sliding_window_prefill_reference_case(cuda):
+    """metal_swa_parity.rs:173-258: four bf16 queries at kv_offset 80 with
+    window 16 each see only the last 16 positions of their causal history."""
+    from velox_amd import ops
+
+    hq, hk, d, ps, mb, p, window = 8, 4, 64, 16, 8, 8, 16
+    scale = 1.0 / np.sqrt(d)
+    q = vxo.round_to(rand_vec(4 * hq * d, 41), vxo.BF16).reshape(4, hq, d)
+    k = vxo.round_to(rand_vec(p * hk * ps * d, 42), vxo.BF16).reshape(p, hk, ps, d)
+    v = vxo.round_to(rand_vec(p * hk * ps * d, 43), vxo.BF16).reshape(p, hk, ps, d)
+    bt = np.arange(mb, dtype=np.uint32).reshape(1, mb)
+    cu, sid, kvo = np.array([0, 4], np.uint32), np.zeros(4, np.uint32), np.array([80], np.uint32)
+    args = (dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(v, torch.bfloat16), u32(bt), u32(cu), u32(sid),
+            u32(kvo), scale)
+    swa = host(ops.paged_prefill_attention(*args, sliding_window=window))
+    glob = host(ops.paged_prefill_attention(*args))
+    cpu = vxo.paged_attention(q, k, v, bt, cu, kvo, scale, sliding_window=window)
+    assert_close("prefill swa", swa, cpu, 3e-2, 3e-2)
+    assert np.abs(glob - swa).max() > 1e-2, "the window did not change the output"
+
+
 def _prefill_case(new_lens, kv_offsets, bt, p, seed, dt="bf16", hq=16, hk=8, d=128, ps=16, tree=None):
     from velox_amd import ops
 
