@@ -13,12 +13,31 @@ _C = 1442695040888963407
 _M = (1 << 64) - 1
 
 
-def rand_vec(n: int, seed: int) -> np.ndarray:
+_BLOCK = 4096
+
+
+def _lcg_states(n: int, seed: int) -> np.ndarray:
+    """States s_1..s_n of s_i = s_{i-1} * A + C (mod 2^64), s_0 = seed * A + C.
+    The first block is stepped one by one; later blocks jump B steps at once
+    (s_{i+B} = A^B s_i + C_B, with numpy's wrapping uint64 arithmetic)."""
+    b = min(n, _BLOCK)
+    out = np.empty(n, np.uint64)
     s = (seed * _A + _C) & _M
-    out = np.empty(n, np.uint32)
-    for i in range(n):
+    for i in range(b):
         s = (s * _A + _C) & _M
-        out[i] = (s >> 33) & 0xFFFFFFFF
+        out[i] = s
+    ab, cb = 1, 0
+    for _ in range(b):
+        ab, cb = (ab * _A) & _M, (cb * _A + _C) & _M
+    ab, cb = np.uint64(ab), np.uint64(cb)
+    for j in range(b, n, b):
+        m = min(b, n - j)
+        out[j:j + m] = out[j - b:j - b + m] * ab + cb
+    return out
+
+
+def rand_vec(n: int, seed: int) -> np.ndarray:
+    out = ((_lcg_states(n, seed) >> np.uint64(33)) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
     # (x as u32 as f32) / (u32::MAX as f32) - 0.5, all in f32
     return (out.astype(np.float32) / np.float32(4294967295.0)) - np.float32(0.5)
 

@@ -60,6 +60,31 @@ def test_qmm_reference_cases(cuda, case):
     assert_close(f"qmm {dt}", host(y), cpu, atol, rtol)
 
 
+QMV_CASES = [  # metal_qmv_mlx_parity.rs:124-155 (M = 1, the draft's matvec), tolerances :99-104
+    ("f32", 4096, 4096, 0x1234, 1e-3, 1e-4),
+    ("f16", 4096, 4096, 0x5678, 5e-2, 5e-3),
+    ("bf16", 4096, 4096, 0xABCD, 5e-1, 1e-2),
+    ("f32", 3072, 3072, 0xFEED, 1e-3, 1e-4),
+    ("f16", 14336, 4096, 0xBEEF, 5e-2, 5e-3),
+    ("f32", 8, 512, 0x1357, 1e-3, 1e-4),
+]
+
+
+@pytest.mark.parametrize("case", QMV_CASES, ids=lambda c: f"{c[0]}-n{c[1]}k{c[2]}")
+def test_qmm_m1_reference_cases(cuda, case):
+    """One-row qmm_4bit against the oracle on the reference's qmv cases
+    (x and w from rand_vec(seed), rand_vec(seed + 1); the oracle takes the
+    unrounded f32 values, as the reference's CPU side does)."""
+    from velox_amd import ops
+
+    dt, n, k, seed, atol, rtol = case
+    x = rand_vec(k, seed).reshape(1, k)
+    qw, sc, bi = quantize_mlx_4bit(rand_vec(n * k, seed + 1), n, k, 64)
+    cpu = vxo.qmm_4bit(x, qw, sc, bi, None, 64, threads=8)
+    y = ops.qmm_4bit(dev(x, TD[dt]), u32(qw), dev(sc, TD[dt]), dev(bi, TD[dt]), None, 64)
+    assert_close(f"qmv {dt} {n}x{k}", host(y), cpu, atol, rtol)
+
+
 def synth_linear(n, k, seed):
     from velox_amd import synth
 
