@@ -20,8 +20,10 @@ def _lcg_states(n: int, seed: int) -> np.ndarray:
     """States s_1..s_n of s_i = s_{i-1} * A + C (mod 2^64), s_0 = seed * A + C.
     The first block is stepped one by one; later blocks jump B steps at once
     (s_{i+B} = A^B s_i + C_B, with numpy's wrapping uint64 arithmetic)."""
-    b = min(n, _BLOCK)
     out = np.empty(n, np.uint64)
+    if n == 0:
+        return out
+    b = min(n, _BLOCK)
     s = (seed * _A + _C) & _M
     for i in range(b):
         s = (s * _A + _C) & _M
