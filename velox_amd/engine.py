@@ -54,9 +54,9 @@ class PagedKvCache:
     def layer_pool_ptr(self, layer, kv):
         return lib.vx_pages_pool(self._h, layer, kv)
 
-    def __del__(self):
+    def __del__(self, _destroy=lib.vx_pages_destroy):  # bound now: module globals may be gone at exit
         if getattr(self, "_h", None):
-            lib.vx_pages_destroy(self._h)
+            _destroy(self._h)
             self._h = None
 
 
@@ -134,9 +134,9 @@ class PagedQwen3:
         """qwen3.rs:1023-1036: logits of every input position."""
         return self._run(pages, input_ids, seqs, True, tree_parents, stream)
 
-    def __del__(self):
+    def __del__(self, _destroy=lib.vx_model_destroy):  # bound now: module globals may be gone at exit
         if getattr(self, "_h", None):
-            lib.vx_model_destroy(self._h)
+            _destroy(self._h)
             self._h = None
 
 
@@ -233,9 +233,9 @@ class SpecEngine:
     def free(self, state):
         lib.vx_spec_free(self._h, state.id)
 
-    def __del__(self):
+    def __del__(self, _destroy=lib.vx_spec_destroy):  # bound now: module globals may be gone at exit
         if getattr(self, "_h", None):
-            lib.vx_spec_destroy(self._h)
+            _destroy(self._h)
             self._h = None
 
 

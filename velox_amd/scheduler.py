@@ -129,9 +129,9 @@ class BatchScheduler:
     def cache_pages(self) -> int:
         return lib.vx_sched_cache_pages(self._h)
 
-    def close(self) -> None:
+    def close(self, _destroy=lib.vx_sched_destroy) -> None:  # bound now: module globals may be gone at exit
         if getattr(self, "_h", None):
-            lib.vx_sched_destroy(self._h)
+            _destroy(self._h)
             self._h = None
 
     def __del__(self):
