@@ -17,6 +17,7 @@ one round of the same workload with a 4-token prompt.
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
   python bench.py --mode qmm   # config 1: isolated verify GEMMs, cache-rotated
   python bench.py --mode continuous   # config 4: scheduler, Qwen3-8B shape
+  python bench.py --mode tree   # config 3: tree verification at context 2048
 """
 from __future__ import annotations
 
@@ -182,7 +183,7 @@ def run_spec(args):
             "ms": agg["verify_ms"], "algorithmic_bytes": verify_bytes, "hbm_gbs": verify_gbs,
             "draft_ms": agg["draft_ms"], "accept_ms": agg["accept_ms"]},
         "roofline": {"bound": "hbm",
-                     "kernel": "qmm_f16_dma_kernel / qmm_f16_k2_kernel: the verify step's int4 GEMMs (36 layers "
+                     "kernel": "qmm_f16_k2_kernel: the verify step's int4 GEMMs (36 layers "
                                "x qkv, o, gate|up with its SwiGLU finish, down; plus the LM head), average per op",
                      "achieved": qmm_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": None if qmm_gbs is None else qmm_gbs / PEAK_HBM_GBS,
@@ -334,6 +335,78 @@ def run_continuous(args):
     print(json.dumps(res), flush=True)
 
 
+def run_tree(args):
+    """Config 3: tree verification on a random-init Qwen3-4B-shaped int4 g64
+    model (seed 3).  16 sequences with 2048-token contexts in paged f16 KV
+    (16-token pages, block tables in shuffled pool order); each step verifies
+    a 16-node draft tree with branching 4-2-2 under the last context token
+    (17 rows per sequence, ancestor-only attention), selects the longest
+    accepted path greedily (vx_accept_tree) and moves that path's K/V rows
+    to consecutive positions (vx_kv_compact_path).  The tree's tokens are
+    synthetic.  Reported: ms per verify step over the whole batch, from the
+    host call of the forward to the end of the compaction."""
+    import torch
+
+    from velox_amd import engine, ops, synth
+
+    torch.cuda.set_device(0)
+    B, ctx, ps = 16, 2048, 16
+    par = [-1, 0, 0, 0, 0] + [p for p in range(1, 5) for _ in range(2)] + [p for p in (5, 6) for _ in range(2)]
+    R = len(par)
+    cfg = synth.qwen3_config("qwen3-4b", max_pos=8192)
+    t0 = time.time()
+    w = synth.host_weights(cfg, seed=3)
+    target = engine.PagedQwen3(cfg, w)
+    del w
+    log(f"[tree] model on device ({time.time() - t0:.1f}s)")
+    V, HK, D = cfg["vocab"], cfg["n_kv_heads"], cfg["head_dim"]
+    need = -(-(ctx - 1 + R) // ps)
+    pool = engine.PagedKvCache(cfg["layers"], HK, D, ps, B * need + 16)
+    rng = np.random.Generator(np.random.Philox(key=[3, 0x74726565]))
+    # allocate every page, then hand them out in shuffled order
+    allp = np.array(pool.alloc(B * need), np.uint32)
+    bts = allp[rng.permutation(allp.size)].reshape(B, need)
+    prompts = [synth.prompt(3, ctx, V, stream=b) for b in range(B)]
+    t1 = time.time()
+    for b0 in range(0, B, 4):  # prefill positions 0..ctx-2 four sequences at a time
+        ids = np.concatenate([prompts[b][:ctx - 1] for b in range(b0, b0 + 4)])
+        target.forward(pool, ids, [(ctx - 1, 0, bts[b]) for b in range(b0, b0 + 4)])
+    torch.cuda.synchronize()
+    log(f"[tree] prefill {B}x{ctx - 1} in {time.time() - t1:.1f}s")
+    nodes = rng.integers(0, V, size=(B, R)).astype(np.uint32)
+    nodes[:, 0] = [prompts[b][ctx - 1] for b in range(B)]
+    ids = nodes.reshape(-1)
+    seqs = [(R, ctx - 1, bts[b]) for b in range(B)]
+    node_dev = torch.from_numpy(nodes.view(np.int32)).cuda()
+    bt_dev = torch.from_numpy(bts.view(np.int32)).cuda()
+    kvo_dev = torch.full((B,), ctx - 1, dtype=torch.int32, device="cuda")
+
+    def step():
+        logits = target.forward_all(pool, ids, seqs, tree_parents=par)
+        acc, path, _ = ops.accept_tree(logits.view(B, R, V), par, node_dev)
+        ops.kv_compact_path(pool, bt_dev, kvo_dev, acc, path)
+        return acc
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ts = time.perf_counter()
+    accepted = 0
+    for _ in range(args.steps):
+        accepted += int(step().sum().item()) + B
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - ts) * 1e3 / args.steps
+    res = {"mode": "tree", "metric": "tree-verify step latency, config 3 (Qwen3-4B shape int4, 16 seqs x ctx 2048, "
+                                      "4-2-2 tree)", "value": ms, "unit": "ms per step", "higher_is_better": False,
+           "rows_per_s": B * R / (ms * 1e-3), "committed_tokens_per_step": accepted / args.steps,
+           "steps": args.steps, "warmup": args.warmup,
+           "config": {"workload": "tree verification + greedy path accept + KV compaction", "batch": B,
+                      "context": ctx, "tree_nodes": R - 1, "branching": "4-2-2", "page_size": ps,
+                      "block_tables": "shuffled"},
+           "data": "synthetic (random-init weights, Philox prompts and tree tokens)"}
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -343,7 +416,7 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=128)
-    ap.add_argument("--mode", choices=["spec", "qmm", "continuous"], default="spec")
+    ap.add_argument("--mode", choices=["spec", "qmm", "continuous", "tree"], default="spec")
     ap.add_argument("--batch-tokens", type=int, default=8192, help="continuous mode: max_batch_tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
@@ -357,6 +430,8 @@ def main():
         run_qmm(args)
     elif args.mode == "continuous":
         run_continuous(args)
+    elif args.mode == "tree":
+        run_tree(args)
     else:
         run_spec(args)
 

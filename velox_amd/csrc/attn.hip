@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "vx_common.h"
 
@@ -700,7 +701,17 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
         VX_HIP(hipGetLastError());
         return 0;
     }
-    const int qn_max = D <= 128 ? 64 : 32;
+    // Query vectors per tile.  Every query tile reads the sequence's whole KV
+    // range, and the 64-vector tile is a heavy kernel (one workgroup per CU).
+    // When a sequence's queries need two 64-vector tiles anyway (65..128, e.g.
+    // a 17-node tree times 4 query heads per KV head), 32-vector tiles are
+    // faster: 11.3 vs 21.6 ms per tree-verify step of 16 x 17 rows at context
+    // 2048.  Long prefill keeps the 64-vector tile (5 % faster there).
+    // VX_ATTN_QN overrides the cap.
+    const char *qn_env = getenv("VX_ATTN_QN");
+    int qn_max = D <= 128 ? 64 : 32;
+    if (qn_max == 64 && max_rows * a.G > 64 && max_rows * a.G <= 128) qn_max = 32;
+    if (qn_env && *qn_env) qn_max = atoi(qn_env);
     int64_t qn = std::min<int64_t>(max_rows * a.G, qn_max);
     int QT = (int)std::max<int64_t>(1, vx_cdiv(qn, 16));
     if (QT == 3) QT = 4;
