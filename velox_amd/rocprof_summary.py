@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 result databases (ROCm 7.x writes SQLite).
 
-    python -m velox_amd.rocprof_summary trace RESULTS.db [--top N]
+    python -m velox_amd.rocprof_summary trace RESULTS.db|run_kernel_trace.csv [--top N]
         per (kernel, grid) dispatch count and duration statistics
     python -m velox_amd.rocprof_summary verify RESULTS.db [--rounds R] [--pmc FILE.db ...]
         the verify int4 GEMMs of the spec bench's timed rounds: every packed
@@ -31,7 +31,15 @@ def _short(name: str) -> str:
 
 def dispatches(db: str):
     """[(short name, start, end, workgroups along x, grid_y, dispatch_id)] in start order
-    (rocprofv3 records grid_x in work-items)."""
+    (rocprofv3 records grid_x in work-items).  db is a results database, or
+    the run_kernel_trace.csv of `--output-format csv`."""
+    if db.endswith(".csv"):
+        import csv
+
+        rows = sorted(csv.DictReader(open(db)), key=lambda r: int(r["Start_Timestamp"]))
+        return [(_short(r["Kernel_Name"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                 int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])), int(r["Grid_Size_Y"]),
+                 int(r["Dispatch_Id"])) for r in rows]
     c = sqlite3.connect(db)
     rows = c.execute("select name, start, end, grid_x, grid_y, dispatch_id, workgroup_x from kernels "
                      "order by start").fetchall()
