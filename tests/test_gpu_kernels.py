@@ -550,6 +550,44 @@ def test_accept_stochastic_config2_bit_exact(cuda, k):
         assert np.array_equal(tk[b, : a + 1], ref_tok[b, : a + 1]), f"seq {b}"
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("V", [300, 8192, 8193, 20000])
+def test_stochastic_draws_edge_cases(cuda, V, dtype):
+    """Vocabularies off the 256 / 8192 grid, uniforms at 0 and just below 1,
+    and peaked rows whose probabilities underflow to 0 outside a few tokens
+    (the walk's fallbacks to the last positive index): draft draws, accepted
+    lengths and tokens bit-identical to the host definition."""
+    from velox_amd import ops
+
+    B, k, T = 6, 3, 0.8
+    rng = np.random.Generator(np.random.Philox(key=[9, V]))
+    tl = rng.normal(0, 3, size=(B, k + 1, V)).astype(np.float32)
+    tl[0] = -60.0
+    tl[0, :, rng.integers(0, V, 3)] = 60.0  # three live tokens per row, the rest exp(-150) -> 0
+    tl[1, :, V - 1] = 40.0                  # mass at the very last index
+    dl = (tl[:, :k] + rng.normal(0, 1, size=(B, k, V))).astype(np.float32)
+    dl[0] = tl[0, :k]
+    if dtype == "bf16":
+        tl, dl = vxo.round_to(tl, vxo.BF16), vxo.round_to(dl, vxo.BF16)
+    uni = vxo.spec_uniforms(9, 0, 0, B, k).copy()
+    top = np.float32(np.nextafter(np.float32(1), np.float32(0)))
+    uni[2, :, :] = 0.0
+    uni[3, :, :] = top
+    uni[4, :, 1] = top  # reject every candidate: residual draws
+    inv_t = np.float32(1.0) / np.float32(T)
+    cand = vxo.sample_draft(dl, uni, inv_t)
+    u_draft = np.ascontiguousarray(uni[:, :k, 0]).reshape(-1)
+    cand_gpu = ops.sample_rows(dev(dl.reshape(B * k, V), TD[dtype]), dev(u_draft), T).cpu().numpy().view(np.uint32)
+    assert np.array_equal(cand_gpu, cand.reshape(-1)), "draft draws must be bit-identical"
+    acc, tok = ops.accept_stochastic(dev(tl, TD[dtype]), dev(dl, TD[dtype]), u32(cand), dev(uni), T)
+    ref_acc, ref_tok = vxo.accept_stochastic(tl, dl, cand, uni, inv_t)
+    assert np.array_equal(acc.cpu().numpy(), ref_acc)
+    tk = tok.cpu().numpy().view(np.uint32)
+    for b in range(B):
+        a = ref_acc[b]
+        assert np.array_equal(tk[b, : a + 1], ref_tok[b, : a + 1]), f"seq {b}"
+
+
 def test_accept_tree_exact(cuda):
     from velox_amd import ops
 

@@ -114,8 +114,8 @@ int sample_rows_launch(const void *logits, int ldt, const float *uni, int64_t us
                        int64_t next_stride, void *ws, size_t ws_bytes, hipStream_t st);
 int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint32_t *cand,
                              const float *uni, int32_t *accepted, uint32_t *tokens, int64_t batch,
-                             int64_t k, int64_t vocab, float temperature, void *ws, size_t ws_bytes,
-                             hipStream_t st);
+                             int64_t k, int64_t vocab, float temperature, bool draft_step_major, void *ws,
+                             size_t ws_bytes, hipStream_t st);
 int embed_launch(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_t rows, int64_t H,
                  int64_t vocab, hipStream_t st);
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
@@ -931,7 +931,6 @@ struct vx_spec {
     DevBuf d_ids, d_cand, d_vids, d_tlog, d_dlog, d_acc, d_tok, d_uni, d_meta, d_argws, d_draw;
     DevBuf d_amax;  // greedy-argmax partials written by the LM heads: values then indices
     DevBuf d_plog;  // prefill-chunk logits (discarded, spec.rs:172-173)
-    DevBuf d_dlog_t;  // stochastic rounds: draft logits as [n][D][V]
     // host staging (pinned)
     void *h_stage = nullptr;
     size_t h_stage_n = 0;
@@ -1310,14 +1309,9 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
                                     (int32_t *)e->d_acc.p, (uint32_t *)e->d_tok.p, nullptr, nullptr, nullptr, nullptr,
                                     0, e->d_argws.p, e->d_argws.n, st));
     } else {
-        // draft logits are laid out [D][n][V]; the acceptance expects [n][D][V]
-        DevBuf &tmp = e->d_dlog_t;
-        VX_TRY(tmp.ensure((size_t)n * D * V * 2));
-        for (int64_t i = 0; i < D; i++)
-            VX_HIP(hipMemcpy2DAsync((uint16_t *)tmp.p + i * V, D * V * 2, (uint16_t *)e->d_dlog.p + (size_t)i * n * V,
-                                    V * 2, V * 2, n, hipMemcpyDeviceToDevice, st));
-        VX_TRY(stochastic_accept_launch(e->d_tlog.p, tmp.p, VX_BF16, cand, uni, (int32_t *)e->d_acc.p,
-                                        (uint32_t *)e->d_tok.p, n, D, V, temp, e->d_argws.p, e->d_argws.n,
+        // draft logits are laid out [D][n][V] (step-major)
+        VX_TRY(stochastic_accept_launch(e->d_tlog.p, e->d_dlog.p, VX_BF16, cand, uni, (int32_t *)e->d_acc.p,
+                                        (uint32_t *)e->d_tok.p, n, D, V, temp, true, e->d_argws.p, e->d_argws.n,
                                         st));
     }
     // ---- results to host (one copy set, one sync)

@@ -467,189 +467,255 @@ __device__ __forceinline__ float resid_elem(const void *lt, float mt, float zt, 
     return d > 0.f ? d : 0.f;
 }
 
-// Inverse-CDF draw over r_j (hierarchical prefix order: chunk -> sub-chunk ->
-// element, each level summed sequentially in index order).  Called by a full
-// 256-thread block; sub-chunk sums use block-wide parallelism (one sub-chunk
-// per thread at a time), the walk itself runs on thread 0.
+// ---- residual / softmax draws ----------------------------------------------
+// Inverse-CDF draw over r_j (p_j, or max(0, p_j - q_j) for a rejection) with
+// the hierarchical prefix order shared with the host definition: 256-element
+// sub-chunks summed sequentially in index order, 32 sub-chunk sums per
+// 8192-element chunk summed in order, chunk sums in order; the walk descends
+// chunk -> sub-chunk -> element.  If rounding leaves the walk short inside a
+// chunk, the draw is the chunk's last index with r_j > 0; if it never crosses
+// the target, the row's last such index (0 if none).
+//
+// Two launches per batch of draws: resid_chunk_kernel (one workgroup per
+// draw and chunk: r_j staged in LDS from coalesced loads, the 32 sub-chunk
+// sums, the chunk sum, the chunk's last positive index) and resid_walk_kernel
+// (one workgroup per draw: the descent, with the selected sub-chunk's r_j
+// recomputed in parallel and walked by one lane).
+constexpr int kSubPerChunk = kSmChunk / kSmSub;  // 32
+constexpr int kMaxChunks = 32;                    // vocab <= 262144
+
+struct DrawDesc {
+    int64_t trow;  // row of the target (or sampled) logits
+    int64_t drow;  // row of the draft logits, -1 = plain softmax draw
+    float mt, zt, md, zd, u;
+    int64_t out;   // index of the drawn token in the token output
+};
+
+struct DrawArgs {
+    const void *tl, *dl;
+    const float *uni;    // SAMPLE: uniforms[row * ustride]
+    int64_t ustride;
+    const float *cm, *cz;  // SAMPLE: chunk statistics of each row
+    int n_chunks;
+    int64_t vocab;
+    float inv_t;
+    DrawDesc *desc;  // [draws]
+    float *ss;       // [draws, n_chunks * 32] sub-chunk sums
+    float *cs;       // [draws, n_chunks] chunk sums
+    int32_t *lastpos;  // [draws, n_chunks] last index with r_j > 0, -1 = none
+    uint32_t *out;     // token output (SAMPLE: [draws]; accept: tokens indexed by desc.out)
+    uint32_t *next_ids;
+    int64_t next_stride;
+};
+
 template <int DT>
-__device__ uint32_t sample_residual_block(const void *lt, float mt, float zt, const void *ld, float md,
-                                          float zd, int64_t vocab, float inv_t, float u, float *ss,
-                                          float *cs, int *s_last_pos, uint32_t *s_out) {
-    const int64_t nch = (vocab + kSmChunk - 1) / kSmChunk;
-    const int64_t nsub_per = kSmChunk / kSmSub;
-    const int64_t nsub = nch * nsub_per;
-    if (threadIdx.x == 0) *s_last_pos = -1;
-    __syncthreads();
-    int my_last = -1;
-    for (int64_t sidx = threadIdx.x; sidx < nsub; sidx += blockDim.x) {
-        const int64_t lo = sidx * kSmSub;
-        float s = 0.f;
-        for (int64_t j = lo; j < lo + kSmSub && j < vocab; j++) {
-            const float r = resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j);
-            if (r > 0.f) my_last = (int)j;
-            s = __fadd_rn(s, r);
+__device__ __forceinline__ const void *row_ptr(const void *base, int64_t row, int64_t vocab) {
+    return (const char *)base + row * vocab * (DT == VX_F32 ? 4 : 2);
+}
+
+// SAMPLE: draw d reads row d; its statistics are combined here and the
+// descriptor is written by chunk 0's workgroup for the walk.
+template <int DT, bool SAMPLE>
+__global__ __launch_bounds__(256) void resid_chunk_kernel(DrawArgs a) {
+    __shared__ float rb[kSmSub * (kSubPerChunk + 1)];  // [position][sub-chunk], padded: conflict-free both ways
+    __shared__ float sub[kSubPerChunk];
+    __shared__ DrawDesc sd;
+    __shared__ int s_last;
+    const int nch = a.n_chunks;
+    const int64_t d = blockIdx.x / nch;
+    const int c = blockIdx.x % nch;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        DrawDesc x;
+        if (SAMPLE) {
+            float M, Z;
+            combine_stats(a.cm + d * nch, a.cz + d * nch, nch, a.inv_t, M, Z);
+            x = {d, -1, M, Z, 0.f, 1.f, a.uni[d * a.ustride], d};
+            if (c == 0) a.desc[d] = x;
+        } else {
+            x = a.desc[d];
         }
-        ss[sidx] = s;
+        sd = x;
+        s_last = -1;
     }
-    atomicMax(s_last_pos, my_last);
     __syncthreads();
-    for (int64_t c = threadIdx.x; c < nch; c += blockDim.x) {
+    const void *lt = row_ptr<DT>(a.tl, sd.trow, a.vocab);
+    const void *ld = sd.drow >= 0 ? row_ptr<DT>(a.dl, sd.drow, a.vocab) : nullptr;
+    const float mt = sd.mt, zt = sd.zt, md = sd.md, zd = sd.zd;
+    const int64_t lo = (int64_t)c * kSmChunk;
+    const int n = (int)min((int64_t)kSmChunk, a.vocab - lo);
+    int my_last = -1;
+#pragma unroll 4
+    for (int i = 0; i < kSubPerChunk; i++) {
+        const int jl = i * kSmSub + tid;
+        float r = 0.f;
+        if (jl < n) {
+            r = resid_elem<DT>(lt, mt, zt, ld, md, zd, a.inv_t, lo + jl);
+            if (r > 0.f) my_last = (int)(lo + jl);
+        }
+        rb[tid * (kSubPerChunk + 1) + i] = r;
+    }
+    atomicMax(&s_last, my_last);
+    __syncthreads();
+    if (tid < kSubPerChunk) {
+        const int cnt = max(0, min(kSmSub, n - tid * kSmSub));
         float s = 0.f;
-        for (int64_t i = 0; i < nsub_per; i++) s = __fadd_rn(s, ss[c * nsub_per + i]);
-        cs[c] = s;
+        for (int p = 0; p < cnt; p++) s = __fadd_rn(s, rb[p * (kSubPerChunk + 1) + tid]);
+        sub[tid] = s;
+        a.ss[(d * nch + c) * kSubPerChunk + tid] = s;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
+        float s = 0.f;
+        for (int i = 0; i < kSubPerChunk; i++) s = __fadd_rn(s, sub[i]);
+        a.cs[d * nch + c] = s;
+        a.lastpos[d * nch + c] = s_last;
+    }
+}
+
+template <int DT, bool SAMPLE>
+__global__ __launch_bounds__(256) void resid_walk_kernel(DrawArgs a) {
+    __shared__ float s_cs[kMaxChunks];
+    __shared__ int s_lp[kMaxChunks];
+    __shared__ float s_ss[kSubPerChunk];
+    __shared__ float rb[kSmSub];
+    __shared__ int s_c, s_s;
+    __shared__ float s_run, s_target;
+    __shared__ uint32_t s_result;
+    const int nch = a.n_chunks;
+    const int64_t d = blockIdx.x;
+    const int tid = threadIdx.x;
+    const DrawDesc x = a.desc[d];
+    if (tid < nch) {
+        s_cs[tid] = a.cs[d * nch + tid];
+        s_lp[tid] = a.lastpos[d * nch + tid];
+    }
+    __syncthreads();
+    if (tid == 0) {
         float total = 0.f;
-        for (int64_t c = 0; c < nch; c++) total = __fadd_rn(total, cs[c]);
-        const float target = __fmul_rn(u, total);
-        uint32_t result = *s_last_pos < 0 ? 0u : (uint32_t)*s_last_pos;
+        int last = -1;
+        for (int c = 0; c < nch; c++) {
+            total = __fadd_rn(total, s_cs[c]);
+            last = max(last, s_lp[c]);
+        }
+        const float target = __fmul_rn(x.u, total);
         float run = 0.f;
-        for (int64_t c = 0; c < nch; c++) {
-            if (__fadd_rn(run, cs[c]) > target) {
-                int64_t found = -1;
-                float run2 = run;
-                for (int64_t i = 0; i < nsub_per && found < 0; i++) {
-                    const int64_t sidx = c * nsub_per + i;
-                    if (__fadd_rn(run2, ss[sidx]) > target) {
-                        float run3 = run2;
-                        const int64_t lo = sidx * kSmSub;
-                        for (int64_t j = lo; j < lo + kSmSub && j < vocab; j++) {
-                            run3 = __fadd_rn(run3, resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j));
-                            if (run3 > target) {
-                                found = j;
-                                break;
-                            }
-                        }
-                        if (found < 0) {
-                            for (int64_t j = (c + 1) * kSmChunk - 1; j >= c * kSmChunk; j--)
-                                if (j < vocab && resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j) > 0.f) {
-                                    found = j;
-                                    break;
-                                }
-                        }
-                        break;
-                    }
-                    run2 = __fadd_rn(run2, ss[sidx]);
-                }
-                if (found < 0) {
-                    for (int64_t j = (c + 1) * kSmChunk - 1; j >= c * kSmChunk; j--)
-                        if (j < vocab && resid_elem<DT>(lt, mt, zt, ld, md, zd, inv_t, j) > 0.f) {
-                            found = j;
-                            break;
-                        }
-                }
-                if (found >= 0) result = (uint32_t)found;
+        int sel = -1;
+        for (int c = 0; c < nch; c++) {
+            if (__fadd_rn(run, s_cs[c]) > target) {
+                sel = c;
                 break;
             }
-            run = __fadd_rn(run, cs[c]);
+            run = __fadd_rn(run, s_cs[c]);
         }
-        *s_out = result;
+        s_c = sel;
+        s_run = run;
+        s_target = target;
+        s_result = last < 0 ? 0u : (uint32_t)last;
     }
     __syncthreads();
-    return *s_out;
-}
-
-constexpr int kMaxSub = 1024;  // supports vocab <= kMaxSub * kSmSub = 262144
-constexpr int kMaxChunks = kMaxSub / (kSmChunk / kSmSub);
-
-// One block per sequence: accept/reject walk + residual or bonus draw.
-template <int DT>
-__global__ __launch_bounds__(256) void stochastic_accept_kernel(
-    const void *tl, const void *dl, const uint32_t *cand, const float *uni, const float *cm_t,
-    const float *cz_t, const float *cm_d, const float *cz_d, int n_chunks, int64_t vocab, int k,
-    float inv_t, int32_t *accepted, uint32_t *tokens) {
-    __shared__ float ss[kMaxSub];
-    __shared__ float cs[kMaxChunks];
-    __shared__ int s_last_pos;
-    __shared__ uint32_t s_out;
-    __shared__ int s_rej;
-    __shared__ float s_stats[4];
-    const int64_t b = blockIdx.x;
-    const size_t esz = DT == VX_F32 ? 4 : 2;
-    int a = 0;
-    for (; a < k; a++) {
-        const int64_t trow = b * (k + 1) + a;
-        const int64_t drow = b * k + a;
-        if (threadIdx.x == 0) {
-            float mt, zt, md, zd;
-            combine_stats(cm_t + trow * n_chunks, cz_t + trow * n_chunks, n_chunks, inv_t, mt, zt);
-            combine_stats(cm_d + drow * n_chunks, cz_d + drow * n_chunks, n_chunks, inv_t, md, zd);
-            const uint32_t c = cand[b * k + a];
-            const float p = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>((const char *)tl + trow * vocab * esz, c), mt), inv_t)), zt);
-            const float q = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>((const char *)dl + drow * vocab * esz, c), md), inv_t)), zd);
-            const float ratio = __fdiv_rn(p, q);
-            const float acc = ratio < 1.0f ? ratio : 1.0f;
-            const float u = uni[(b * (k + 1) + a) * 4 + 1];
-            s_rej = !(u < acc);
-            s_stats[0] = mt;
-            s_stats[1] = zt;
-            s_stats[2] = md;
-            s_stats[3] = zd;
-            if (!s_rej) tokens[b * (k + 1) + a] = c;
+    const int c = s_c;
+    if (c >= 0) {  // uniform across the block
+        if (tid < kSubPerChunk) s_ss[tid] = a.ss[(d * nch + c) * kSubPerChunk + tid];
+        __syncthreads();
+        if (tid == 0) {
+            float run = s_run;
+            int sel = -1;
+            for (int i = 0; i < kSubPerChunk; i++) {
+                if (__fadd_rn(run, s_ss[i]) > s_target) {
+                    sel = i;
+                    break;
+                }
+                run = __fadd_rn(run, s_ss[i]);
+            }
+            s_s = sel;
+            s_run = run;
         }
         __syncthreads();
-        if (s_rej) {
-            const uint32_t nxt = sample_residual_block<DT>(
-                (const char *)tl + trow * vocab * esz, s_stats[0], s_stats[1],
-                (const char *)dl + drow * vocab * esz, s_stats[2], s_stats[3], vocab, inv_t,
-                uni[(b * (k + 1) + a) * 4 + 2], ss, cs, &s_last_pos, &s_out);
-            if (threadIdx.x == 0) {
-                tokens[b * (k + 1) + a] = nxt;
-                accepted[b] = a;
+        const int s = s_s;
+        const int64_t lo = ((int64_t)c * kSubPerChunk + max(s, 0)) * kSmSub;
+        const int cnt = (int)min((int64_t)kSmSub, a.vocab - lo);
+        if (s >= 0 && tid < cnt) {
+            const void *lt = row_ptr<DT>(a.tl, x.trow, a.vocab);
+            const void *ld = x.drow >= 0 ? row_ptr<DT>(a.dl, x.drow, a.vocab) : nullptr;
+            rb[tid] = resid_elem<DT>(lt, x.mt, x.zt, ld, x.md, x.zd, a.inv_t, lo + tid);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int64_t found = -1;
+            if (s >= 0) {
+                float run = s_run;
+                for (int p = 0; p < cnt; p++) {
+                    run = __fadd_rn(run, rb[p]);
+                    if (run > s_target) {
+                        found = lo + p;
+                        break;
+                    }
+                }
             }
+            if (found < 0) found = s_lp[c];
+            if (found >= 0) s_result = (uint32_t)found;
+        }
+    }
+    if (tid == 0) {
+        const uint32_t t = s_result;
+        if (SAMPLE) {
+            a.out[d] = t;
+            if (a.next_ids) a.next_ids[d * a.next_stride] = t;
+        } else {
+            a.out[x.out] = t;
+        }
+    }
+}
+
+// One lane per sequence: the accept/reject walk over the k candidates; the
+// accepted candidates are written, and the descriptor of the one draw that
+// follows (residual row at the first rejection, else the bonus row).
+// Draft row of (b, i): b * k + i, or i * batch + b when draft_step_major.
+__global__ __launch_bounds__(64) void stochastic_walk_kernel(
+    const void *tl, const void *dl, int ldt, const uint32_t *cand, const float *uni, const float *cm_t,
+    const float *cz_t, const float *cm_d, const float *cz_d, int n_chunks, int64_t vocab, int k, int64_t batch,
+    int draft_step_major, float inv_t, int32_t *accepted, uint32_t *tokens, DrawDesc *desc) {
+    const int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (b >= batch) return;
+    const size_t esz = ldt == VX_F32 ? 4 : 2;
+    for (int i = 0; i < k; i++) {
+        const int64_t trow = b * (k + 1) + i;
+        const int64_t drow = draft_step_major ? i * batch + b : b * k + i;
+        float mt, zt, md, zd;
+        combine_stats(cm_t + trow * n_chunks, cz_t + trow * n_chunks, n_chunks, inv_t, mt, zt);
+        combine_stats(cm_d + drow * n_chunks, cz_d + drow * n_chunks, n_chunks, inv_t, md, zd);
+        const uint32_t c = cand[b * k + i];
+        const void *tr = (const char *)tl + trow * vocab * esz;
+        const void *dr = (const char *)dl + drow * vocab * esz;
+        float lt_c, ld_c;
+        if (ldt == VX_BF16) {
+            lt_c = ld_elem<VX_BF16>(tr, c);
+            ld_c = ld_elem<VX_BF16>(dr, c);
+        } else if (ldt == VX_F16) {
+            lt_c = ld_elem<VX_F16>(tr, c);
+            ld_c = ld_elem<VX_F16>(dr, c);
+        } else {
+            lt_c = ld_elem<VX_F32>(tr, c);
+            ld_c = ld_elem<VX_F32>(dr, c);
+        }
+        const float p = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(lt_c, mt), inv_t)), zt);
+        const float q = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_c, md), inv_t)), zd);
+        const float ratio = __fdiv_rn(p, q);
+        const float acc = ratio < 1.0f ? ratio : 1.0f;
+        if (!(uni[trow * 4 + 1] < acc)) {
+            desc[b] = {trow, drow, mt, zt, md, zd, uni[trow * 4 + 2], trow};
+            accepted[b] = i;
             return;
         }
-        __syncthreads();
+        tokens[trow] = c;
     }
     const int64_t trow = b * (k + 1) + k;
-    if (threadIdx.x == 0) {
-        float mt, zt;
-        combine_stats(cm_t + trow * n_chunks, cz_t + trow * n_chunks, n_chunks, inv_t, mt, zt);
-        s_stats[0] = mt;
-        s_stats[1] = zt;
-    }
-    __syncthreads();
-    const uint32_t nxt = sample_residual_block<DT>((const char *)tl + trow * vocab * esz, s_stats[0], s_stats[1],
-                                                   nullptr, 0.f, 1.f, vocab, inv_t,
-                                                   uni[(b * (k + 1) + k) * 4 + 2], ss, cs, &s_last_pos, &s_out);
-    if (threadIdx.x == 0) {
-        tokens[b * (k + 1) + k] = nxt;
-        accepted[b] = k;
-    }
+    float mt, zt;
+    combine_stats(cm_t + trow * n_chunks, cz_t + trow * n_chunks, n_chunks, inv_t, mt, zt);
+    desc[b] = {trow, -1, mt, zt, 0.f, 1.f, uni[trow * 4 + 2], trow};
+    accepted[b] = k;
 }
-
-// One block per row: draw from softmax(row / T) with uniforms[row * stride].
-template <int DT>
-__global__ __launch_bounds__(256) void sample_rows_kernel(const void *logits, const float *uni,
-                                                          int64_t ustride, const float *cm,
-                                                          const float *cz, int n_chunks,
-                                                          int64_t vocab, float inv_t,
-                                                          uint32_t *out, uint32_t *next_ids,
-                                                          int64_t next_stride) {
-    __shared__ float ss[kMaxSub];
-    __shared__ float cs[kMaxChunks];
-    __shared__ int s_last_pos;
-    __shared__ uint32_t s_out;
-    __shared__ float s_st[2];
-    const int64_t row = blockIdx.x;
-    if (threadIdx.x == 0) {
-        float M, Z;
-        combine_stats(cm + row * n_chunks, cz + row * n_chunks, n_chunks, inv_t, M, Z);
-        s_st[0] = M;
-        s_st[1] = Z;
-    }
-    __syncthreads();
-    const size_t esz = DT == VX_F32 ? 4 : 2;
-    const uint32_t t = sample_residual_block<DT>((const char *)logits + row * vocab * esz, s_st[0], s_st[1],
-                                                 nullptr, 0.f, 1.f, vocab, inv_t, uni[row * ustride],
-                                                 ss, cs, &s_last_pos, &s_out);
-    if (threadIdx.x == 0) {
-        out[row] = t;
-        if (next_ids) next_ids[row * next_stride] = t;
-    }
-}
-
 }  // namespace vx
 
 using namespace vx;
@@ -734,10 +800,36 @@ int argmax_accept_partials_launch(const float *pv, const uint32_t *pi, int n_chu
     return 0;
 }
 
-// Statistics live after the arrival-counter region so that argmax / accept
-// launches sharing the same workspace keep their zeroed counters.
+// Workspace of the stochastic paths, after the arrival-counter region (so
+// argmax / accept launches sharing the workspace keep their zeroed
+// counters): chunk statistics of `stat_rows` rows, then `draws` descriptors,
+// sub-chunk sums, chunk sums and last positive indices.
+struct StochLayout {
+    float *cm, *cz;
+    DrawDesc *desc;
+    float *ss, *cs;
+    int32_t *lastpos;
+};
+
+static size_t stoch_layout(void *ws, int64_t stat_rows, int64_t draws, int nch, StochLayout *L) {
+    size_t off = kAccCounterBytes;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = (off + bytes + 255) & ~(size_t)255;
+        return (char *)ws + at;
+    };
+    char *cm = take((size_t)stat_rows * nch * 4);
+    char *cz = take((size_t)stat_rows * nch * 4);
+    char *desc = take((size_t)draws * sizeof(DrawDesc));
+    char *ss = take((size_t)draws * nch * kSubPerChunk * 4);
+    char *cs = take((size_t)draws * nch * 4);
+    char *lp = take((size_t)draws * nch * 4);
+    if (L) *L = {(float *)cm, (float *)cz, (DrawDesc *)desc, (float *)ss, (float *)cs, (int32_t *)lp};
+    return off;
+}
+
 size_t stochastic_workspace_bytes(int64_t rows, int64_t vocab) {
-    return kAccCounterBytes + (size_t)rows * vx_cdiv(vocab, kSmChunk) * 8 + 256;
+    return stoch_layout(nullptr, rows, rows, (int)vx_cdiv(vocab, kSmChunk), nullptr);
 }
 
 template <int DT>
@@ -757,11 +849,27 @@ static void stats(const void *lg, int ldt, int64_t rows, int64_t vocab, float in
         launch_stats<VX_F32>(lg, rows, vocab, inv_t, cm, cz, nch, st);
 }
 
+template <int DT, bool SAMPLE>
+static void launch_draws_dt(const DrawArgs &a, int64_t draws, hipStream_t st) {
+    hipLaunchKernelGGL((resid_chunk_kernel<DT, SAMPLE>), dim3((unsigned)(draws * a.n_chunks)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((resid_walk_kernel<DT, SAMPLE>), dim3((unsigned)draws), dim3(256), 0, st, a);
+}
+
+template <bool SAMPLE>
+static void launch_draws(const DrawArgs &a, int ldt, int64_t draws, hipStream_t st) {
+    if (ldt == VX_BF16)
+        launch_draws_dt<VX_BF16, SAMPLE>(a, draws, st);
+    else if (ldt == VX_F16)
+        launch_draws_dt<VX_F16, SAMPLE>(a, draws, st);
+    else
+        launch_draws_dt<VX_F32, SAMPLE>(a, draws, st);
+}
+
 int sample_rows_launch(const void *logits, int ldt, const float *uni, int64_t ustride, uint32_t *out,
                        int64_t rows, int64_t vocab, float temperature, uint32_t *next_ids,
                        int64_t next_stride, void *ws, size_t ws_bytes, hipStream_t st) {
     VX_REQUIRE(temperature > 0.f, "sample: temperature must be > 0");
-    VX_REQUIRE(vocab <= (int64_t)kMaxSub * kSmSub, "sample: vocab too large");
+    VX_REQUIRE(vocab > 0 && vocab <= (int64_t)kMaxChunks * kSmChunk, "sample: vocab must be 1..262144");
     const int nch = (int)vx_cdiv(vocab, kSmChunk);
     const size_t need = stochastic_workspace_bytes(rows, vocab);
     if (!ws) {
@@ -769,27 +877,24 @@ int sample_rows_launch(const void *logits, int ldt, const float *uni, int64_t us
     } else if (ws_bytes < need) {
         return set_error("sample: workspace too small");
     }
-    float *cm = (float *)((char *)ws + kAccCounterBytes);
-    float *cz = cm + rows * nch;
+    StochLayout L;
+    stoch_layout(ws, rows, rows, nch, &L);
     const float inv_t = 1.0f / temperature;
-    stats(logits, ldt, rows, vocab, inv_t, cm, cz, nch, st);
-    if (ldt == VX_BF16)
-        hipLaunchKernelGGL(sample_rows_kernel<VX_BF16>, dim3((unsigned)rows), dim3(256), 0, st, logits, uni, ustride, cm, cz, nch, vocab, inv_t, out, next_ids, next_stride);
-    else if (ldt == VX_F16)
-        hipLaunchKernelGGL(sample_rows_kernel<VX_F16>, dim3((unsigned)rows), dim3(256), 0, st, logits, uni, ustride, cm, cz, nch, vocab, inv_t, out, next_ids, next_stride);
-    else
-        hipLaunchKernelGGL(sample_rows_kernel<VX_F32>, dim3((unsigned)rows), dim3(256), 0, st, logits, uni, ustride, cm, cz, nch, vocab, inv_t, out, next_ids, next_stride);
+    stats(logits, ldt, rows, vocab, inv_t, L.cm, L.cz, nch, st);
+    DrawArgs a{logits, nullptr, uni, ustride, L.cm, L.cz, nch, vocab, inv_t, L.desc, L.ss, L.cs, L.lastpos,
+               out, next_ids, next_stride};
+    launch_draws<true>(a, ldt, rows, st);
     VX_HIP(hipGetLastError());
     return 0;
 }
 
 int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint32_t *cand,
                              const float *uni, int32_t *accepted, uint32_t *tokens, int64_t batch,
-                             int64_t k, int64_t vocab, float temperature, void *ws, size_t ws_bytes,
-                             hipStream_t st) {
+                             int64_t k, int64_t vocab, float temperature, bool draft_step_major, void *ws,
+                             size_t ws_bytes, hipStream_t st) {
     VX_REQUIRE(temperature > 0.f, "accept_stochastic: temperature must be > 0");
     VX_REQUIRE(k >= 1, "accept_stochastic: k must be >= 1");
-    VX_REQUIRE(vocab <= (int64_t)kMaxSub * kSmSub, "accept_stochastic: vocab too large");
+    VX_REQUIRE(vocab > 0 && vocab <= (int64_t)kMaxChunks * kSmChunk, "accept_stochastic: vocab must be 1..262144");
     const int nch = (int)vx_cdiv(vocab, kSmChunk);
     const int64_t trows = batch * (k + 1), drows = batch * k;
     const size_t need = stochastic_workspace_bytes(trows + drows, vocab);
@@ -798,19 +903,18 @@ int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint
     } else if (ws_bytes < need) {
         return set_error("accept_stochastic: workspace too small");
     }
-    float *cm_t = (float *)((char *)ws + kAccCounterBytes);
-    float *cz_t = cm_t + trows * nch;
-    float *cm_d = cz_t + trows * nch;
-    float *cz_d = cm_d + drows * nch;
+    StochLayout L;
+    stoch_layout(ws, trows + drows, batch, nch, &L);
+    float *cm_d = L.cm + trows * nch, *cz_d = L.cz + trows * nch;
     const float inv_t = 1.0f / temperature;
-    stats(tl, ldt, trows, vocab, inv_t, cm_t, cz_t, nch, st);
+    stats(tl, ldt, trows, vocab, inv_t, L.cm, L.cz, nch, st);
     stats(dl, ldt, drows, vocab, inv_t, cm_d, cz_d, nch, st);
-    if (ldt == VX_BF16)
-        hipLaunchKernelGGL(stochastic_accept_kernel<VX_BF16>, dim3((unsigned)batch), dim3(256), 0, st, tl, dl, cand, uni, cm_t, cz_t, cm_d, cz_d, nch, vocab, (int)k, inv_t, accepted, tokens);
-    else if (ldt == VX_F16)
-        hipLaunchKernelGGL(stochastic_accept_kernel<VX_F16>, dim3((unsigned)batch), dim3(256), 0, st, tl, dl, cand, uni, cm_t, cz_t, cm_d, cz_d, nch, vocab, (int)k, inv_t, accepted, tokens);
-    else
-        hipLaunchKernelGGL(stochastic_accept_kernel<VX_F32>, dim3((unsigned)batch), dim3(256), 0, st, tl, dl, cand, uni, cm_t, cz_t, cm_d, cz_d, nch, vocab, (int)k, inv_t, accepted, tokens);
+    hipLaunchKernelGGL(stochastic_walk_kernel, dim3((unsigned)vx_cdiv(batch, 64)), dim3(64), 0, st, tl, dl, ldt,
+                       cand, uni, L.cm, L.cz, cm_d, cz_d, nch, vocab, (int)k, batch, (int)draft_step_major, inv_t,
+                       accepted, tokens, L.desc);
+    DrawArgs a{tl, dl, nullptr, 0, nullptr, nullptr, nch, vocab, inv_t, L.desc, L.ss, L.cs, L.lastpos,
+               tokens, nullptr, 0};
+    launch_draws<false>(a, ldt, batch, st);
     VX_HIP(hipGetLastError());
     return 0;
 }
@@ -963,7 +1067,7 @@ extern "C" int vx_accept_stochastic(const void *target_logits, const void *draft
                "accept_stochastic: null tensor");
     if (batch == 0) return 0;
     return stochastic_accept_launch(target_logits, draft_logits, logits_dtype, candidates, uniforms, accepted,
-                                    tokens, batch, k, vocab, temperature, workspace, workspace_bytes,
+                                    tokens, batch, k, vocab, temperature, false, workspace, workspace_bytes,
                                     (hipStream_t)stream);
 }
 
