@@ -18,6 +18,7 @@ one round of the same workload with a 4-token prompt.
   python bench.py --mode qmm   # config 1: isolated verify GEMMs, cache-rotated
   python bench.py --mode continuous   # config 4: scheduler, Qwen3-8B shape
   python bench.py --mode tree   # config 3: tree verification at context 2048
+  python bench.py --mode config0   # config 0 end to end, GPU and CPU oracle
 """
 from __future__ import annotations
 
@@ -318,6 +319,83 @@ def run_qmm(args):
           flush=True)
 
 
+def run_config0(args):
+    """Config 0, the reference's CPU-runnable case, end to end: greedy spec
+    decode on a random-init Qwen3-0.6B-shaped int4 g64 model (seed 0), batch 1,
+    draft = the target's first 4 layers, a 128-token uniform-random prompt,
+    k = 4, 64 generated tokens.  The GPU engine and the CPU oracle (the
+    reference's spec loop restated, OpenMP) run the identical workload; each
+    reports generated tokens / wall time of its rounds (prefill excluded), and
+    the two token streams are compared.  The GPU figure is the second of two
+    runs (the first warms the allocator and code objects)."""
+    import torch
+
+    from velox_amd import engine, synth
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import vxo
+
+    torch.cuda.set_device(0)
+    k, n_new, plen = 4, 64, 128
+    cfg = synth.qwen3_config("qwen3-0.6b", max_pos=4096)
+    w = synth.host_weights(cfg, seed=0)
+    prompt = synth.prompt(0, plen, cfg["vocab"])
+    L, HK, D = cfg["layers"], cfg["n_kv_heads"], cfg["head_dim"]
+    pages = (plen + n_new + 2 * (k + 1) + 15) // 16 + 4
+    target = engine.PagedQwen3(cfg, w)
+    draft = engine.PagedQwen3(cfg, w, n_layers=4)
+
+    def gpu_run():
+        e = engine.SpecEngine(target, engine.PagedKvCache(L, HK, D, 16, pages), draft,
+                              engine.PagedKvCache(4, HK, D, 16, pages))
+        st = e.prefill_batch([prompt])
+        torch.cuda.synchronize()
+        toks, acc, rounds = [], 0, 0
+        t0 = time.perf_counter()
+        while len(toks) < n_new:
+            out = e.step_batch(st, k)[0]
+            toks += out.committed_tokens
+            acc += out.accepted
+            rounds += 1
+        torch.cuda.synchronize()
+        return toks, acc, rounds, time.perf_counter() - t0
+
+    gpu_run()
+    g_toks, g_acc, g_rounds, g_s = gpu_run()
+    log(f"[config0] gpu: {len(g_toks)} tokens in {g_rounds} rounds, {g_s * 1e3:.1f} ms")
+    threads = min(16, os.cpu_count() or 1)
+    wt = synth.as_model_dtype(w, "bf16")
+    ocfg = dict(cfg, dtype=vxo.BF16)
+    oe = vxo.SpecEngine(vxo.Model(ocfg, wt, threads=threads), vxo.Pages(L, HK, D, 16, pages),
+                        vxo.Model(ocfg, wt, n_layers=4, threads=threads), vxo.Pages(4, HK, D, 16, pages))
+    t0 = time.perf_counter()
+    ost = oe.prefill([prompt])
+    log(f"[config0] cpu prefill {time.perf_counter() - t0:.1f}s")
+    c_toks, c_acc, c_rounds = [], 0, 0
+    t0 = time.perf_counter()
+    while len(c_toks) < n_new:
+        out = oe.step(ost, k)
+        c_toks += [int(t) for t in out["committed"][0]]
+        c_acc += int(out["accepted"][0])
+        c_rounds += 1
+    c_s = time.perf_counter() - t0
+    log(f"[config0] cpu: {len(c_toks)} tokens in {c_rounds} rounds, {c_s:.1f} s")
+    same = 0
+    while same < min(n_new, len(g_toks), len(c_toks)) and g_toks[same] == c_toks[same]:
+        same += 1
+    res = {"mode": "config0", "metric": "accepted tok/s, Qwen3-0.6B-shape int4 k=4 batch 1 (config 0)",
+           "workload": "greedy spec decode, Qwen3-0.6B shape int4 g64 seed 0, draft = first 4 layers, "
+                       "128-token prompt, k=4, 64 new tokens, batch 1",
+           "gpu": {"value": len(g_toks) / g_s, "unit": "accepted tok/s", "tokens": len(g_toks),
+                   "rounds": g_rounds, "seconds": g_s, "acceptance_rate": g_acc / (g_rounds * k)},
+           "cpu_baseline": {"value": len(c_toks) / c_s, "unit": "accepted tok/s", "tokens": len(c_toks),
+                            "rounds": c_rounds, "seconds": c_s, "acceptance_rate": c_acc / (c_rounds * k),
+                            "cores": threads, "kind": "port",
+                            "sample": "the full config-0 workload on the oracle (oracle/vxo.c, OpenMP)"},
+           "streams": {"tokens_compared": n_new, "identical_leading_tokens": same}}
+    print(json.dumps(res), flush=True)
+
+
 def run_continuous(args):
     """Config 4: continuous-batching speculative decoding on a random-init
     Qwen3-8B-shaped int4 g64 model: 32 requests, prompt lengths U[256, 4096]
@@ -488,7 +566,7 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=128)
-    ap.add_argument("--mode", choices=["spec", "qmm", "continuous", "tree"], default="spec")
+    ap.add_argument("--mode", choices=["spec", "qmm", "continuous", "tree", "config0"], default="spec")
     ap.add_argument("--batch-tokens", type=int, default=8192, help="continuous mode: max_batch_tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
@@ -504,6 +582,8 @@ def main():
         run_continuous(args)
     elif args.mode == "tree":
         run_tree(args)
+    elif args.mode == "config0":
+        run_config0(args)
     else:
         run_spec(args)
 
