@@ -116,8 +116,8 @@ int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint
                              const float *uni, int32_t *accepted, uint32_t *tokens, int64_t batch,
                              int64_t k, int64_t vocab, float temperature, bool draft_step_major, void *ws,
                              size_t ws_bytes, hipStream_t st);
-int embed_launch(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_t rows, int64_t H,
-                 int64_t vocab, hipStream_t st);
+int embed_rmsnorm_launch(const uint32_t *ids, const uint16_t *embed, int64_t vocab, const uint16_t *w,
+                         uint16_t *h, uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
                    int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
 int qkv_partial_rope_scatter_launch(const float *partial, int splits, const uint16_t *qn, const uint16_t *kn,
@@ -390,6 +390,7 @@ struct DevBuf {
 struct Meta {
     int64_t rows = 0, n_seqs = 0, max_blocks = 1, max_rows = 1, max_kv = 1;
     bool tree = false;
+    bool one_row = false;  // every sequence brings exactly one row (row s is its last row)
     // offsets (bytes) inside the blob
     size_t o_pos, o_page, o_slot, o_cu, o_kvo, o_bt, o_mask, o_last, size;
 };
@@ -626,6 +627,7 @@ int build_meta(const vx_model *m, const vx_pages *pg, const SeqDesc *seqs, int64
     }
     meta.rows = rows;
     meta.tree = parents != nullptr;
+    meta.one_row = n > 0 && rows == n && meta.max_rows == 1;
     const int64_t R = n ? seqs[0].new_tokens : 0;
     if (parents && R > 64) return set_error("forward: tree larger than 64 nodes");
     uint64_t tmask[64] = {0};
@@ -768,10 +770,6 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     uint16_t *q = (uint16_t *)m->q.p, *attn = (uint16_t *)m->attn.p, *act = (uint16_t *)m->act.p;
     const float scale = 1.0f / sqrtf((float)D);
 
-    {
-        ProfScope ps_(prof, st, PC_OTHER, 0.0);
-        VX_TRY(embed_launch(ids_dev, m->embed, h, R, H, c.vocab, st));
-    }
     // Per layer: qkv projection (split partials) -> q/k norm + RoPE + KV write
     // (finishing the projection) -> attention -> o projection (partials) ->
     // residual + ln2 norm -> gate|up with the SwiGLU finish -> down
@@ -779,7 +777,7 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     // or the final norm when every row goes to the LM head).
     {
         ProfScope ps_(prof, st, PC_OTHER, 0.0);
-        VX_TRY(rmsnorm_launch(h, m->layers[0].ln1, xn, nullptr, R, H, eps, VX_F16, st));
+        VX_TRY(embed_rmsnorm_launch(ids_dev, m->embed, c.vocab, m->layers[0].ln1, h, xn, R, H, eps, VX_F16, st));
     }
     int splits = 0;
     const float *part = nullptr;
@@ -789,6 +787,11 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     // slower at the bench shape (27.7 us against 5.4 + 11.0 us): the
     // finish adds four dependent memory round trips ahead of the key loop on
     // 128 workgroups, where the separate kernel spreads them over the chip.
+    // The final norm runs inside the last layer's residual kernel when every
+    // row goes to the LM head: all rows, or one row per sequence (a draft
+    // step, where row s is sequence s's last row); otherwise a gather of the
+    // last rows follows the layers.
+    const bool norm_all = all_rows || meta.one_row;
     const int64_t G = HQ / HK;
     const char *fz_env = getenv("VX_FUSED_QKV");
     const bool fuse_qkv = meta.max_rows * G <= (D <= 128 ? 64 : 32) && fz_env && atoi(fz_env) != 0;
@@ -841,13 +844,13 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
         {
             ProfScope ps_(prof, st, PC_OTHER, 0.0);
             const bool last_layer = l + 1 == m->L;
-            const uint16_t *next_ln = !last_layer ? m->layers[l + 1].ln1 : (all_rows ? m->norm : nullptr);
+            const uint16_t *next_ln = !last_layer ? m->layers[l + 1].ln1 : (norm_all ? m->norm : nullptr);
             VX_TRY(residual_rmsnorm_launch(part, splits, ldexpf(1.0f, kMlpShift), h, next_ln, xn, R, H, eps,
                                            VX_F16, st));
         }
     }
     const int64_t lrows = all_rows ? R : meta.n_seqs;
-    if (!all_rows) {
+    if (!norm_all) {
         ProfScope ps_(prof, st, PC_OTHER, 0.0);
         VX_TRY(rmsnorm_launch(h, m->norm, xn, last, lrows, H, eps, VX_F16, st));
     }

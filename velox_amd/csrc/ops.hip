@@ -14,16 +14,6 @@ namespace vx {
 // ===========================================================================
 
 // h[r, :] = round_T(embed[ids[r], :]); embed is stored in T already.
-__global__ void embed_kernel(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_t H,
-                             int64_t vocab) {
-    const int64_t r = blockIdx.x;
-    uint32_t id = ids[r];
-    if (id >= (uint32_t)vocab) id = (uint32_t)(vocab - 1);
-    const uint4 *src = (const uint4 *)(embed + (int64_t)id * H);
-    uint4 *dst = (uint4 *)(h + r * H);
-    for (int64_t i = threadIdx.x; i < H / 8; i += blockDim.x) dst[i] = src[i];
-}
-
 constexpr int kMaxFusedSplits = 8;  // split partials a fused finish reads
 
 // Sum over the workgroup (threads = 64 * waves <= 1024), same value in every thread.
@@ -66,16 +56,21 @@ __device__ __forceinline__ uint4 rms_apply8(const float (&x)[8], uint4 wv, float
 
 // y = round_bf16(x / sqrt(mean(x^2) + eps) * w) (candle RmsNorm in bf16), x, w
 // bf16, y as f16 carrier or bf16.  Rows optionally gathered through row_idx
-// (last row per sequence).  One workgroup per row, one thread per 8 columns;
-// the row and the weights are requested together up front.
+// (the last row per sequence, or token ids into the embedding table: indices
+// clamp to src_rows - 1), and the gathered rows optionally copied to xcopy
+// (the embedding lookup, qwen3.rs:998, fused with the first layer's norm).
+// One workgroup per row, one thread per 8 columns; the row and the weights
+// are requested together up front.
 __global__ __launch_bounds__(1024) void rmsnorm_bf16_kernel(const uint16_t *x, const uint16_t *w, uint16_t *y,
-                                                           const uint32_t *row_idx, int H, float eps, int out_dt) {
+                                                           const uint32_t *row_idx, int H, float eps, int out_dt,
+                                                           int64_t src_rows, uint16_t *xcopy) {
     __shared__ float red[16];
     const int r = blockIdx.x;
     const int i = threadIdx.x;
     const bool live = i < H / 8;
-    const int64_t src_r = row_idx ? row_idx[r] : r;
+    const int64_t src_r = row_idx ? std::min<int64_t>(row_idx[r], src_rows - 1) : r;
     const uint4 xv = live ? ((const uint4 *)(x + src_r * H))[i] : make_uint4(0u, 0u, 0u, 0u);
+    if (xcopy && live) ((uint4 *)(xcopy + (int64_t)r * H))[i] = xv;
     const uint4 wv = live ? ((const uint4 *)w)[i] : make_uint4(0u, 0u, 0u, 0u);
     float f[8];
     bf16x8_unpack(xv, f);
@@ -920,20 +915,27 @@ int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint
 }
 
 // ---- engine helpers --------------------------------------------------------
-int embed_launch(const uint32_t *ids, const uint16_t *embed, uint16_t *h, int64_t rows, int64_t H,
-                 int64_t vocab, hipStream_t st) {
-    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)rows), dim3(64), 0, st, ids, embed, h, H, vocab);
-    VX_HIP(hipGetLastError());
-    return 0;
-}
-
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
                    int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st) {
     if (H % 8 != 0 || H > 8 * 1024) return set_error("rmsnorm: hidden size must be a multiple of 8 and <= 8192");
     if (rows == 0) return 0;
     const unsigned threads = (unsigned)vx_cdiv(H / 8, 64) * 64;
     hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(threads), 0, st, x, w, y, row_idx, (int)H,
-                       eps, out_dt);
+                       eps, out_dt, INT64_MAX, (uint16_t *)nullptr);
+    VX_HIP(hipGetLastError());
+    return 0;
+}
+
+// Embedding lookup fused with the first layer's norm: h[r] = embed[ids[r]]
+// (ids clamped to the vocabulary) and y[r] = RMSNorm(h[r]) * w.
+int embed_rmsnorm_launch(const uint32_t *ids, const uint16_t *embed, int64_t vocab, const uint16_t *w,
+                         uint16_t *h, uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st) {
+    if (H % 8 != 0 || H > 8 * 1024) return set_error("rmsnorm: hidden size must be a multiple of 8 and <= 8192");
+    if (vocab < 1) return set_error("embedding: empty vocabulary");
+    if (rows == 0) return 0;
+    const unsigned threads = (unsigned)vx_cdiv(H / 8, 64) * 64;
+    hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(threads), 0, st, embed, w, y, ids, (int)H,
+                       eps, out_dt, vocab, h);
     VX_HIP(hipGetLastError());
     return 0;
 }
