@@ -116,8 +116,9 @@ int stochastic_accept_launch(const void *tl, const void *dl, int ldt, const uint
                              const float *uni, int32_t *accepted, uint32_t *tokens, int64_t batch,
                              int64_t k, int64_t vocab, float temperature, bool draft_step_major, void *ws,
                              size_t ws_bytes, hipStream_t st);
-int embed_rmsnorm_launch(const uint32_t *ids, const uint16_t *embed, int64_t vocab, const uint16_t *w,
-                         uint16_t *h, uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
+int embed_rmsnorm_launch(const uint32_t *ids, int64_t ids_stride, const uint16_t *embed, int64_t vocab,
+                         const uint16_t *w, uint16_t *h, uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt,
+                         hipStream_t st);
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint32_t *row_idx,
                    int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st);
 int qkv_partial_rope_scatter_launch(const float *partial, int splits, const uint16_t *qn, const uint16_t *kn,
@@ -749,7 +750,7 @@ size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int
 int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &meta, const uint8_t *meta_dev,
                 int all_rows, void *logits, void *ws, size_t ws_bytes, hipStream_t st, Prof *prof = nullptr,
                 double kv_bytes_per_layer = 0.0, float *amax_v = nullptr, uint32_t *amax_i = nullptr,
-                bool *amax_done = nullptr) {
+                bool *amax_done = nullptr, int64_t ids_stride = 1) {
     if (amax_done) *amax_done = false;
     const vx_qwen3_config &c = m->cfg;
     const int64_t H = c.hidden, F = c.inter, D = c.head_dim, HQ = c.n_heads, HK = c.n_kv_heads;
@@ -777,7 +778,8 @@ int forward_dev(vx_model *m, vx_pages *pg, const uint32_t *ids_dev, const Meta &
     // or the final norm when every row goes to the LM head).
     {
         ProfScope ps_(prof, st, PC_OTHER, 0.0);
-        VX_TRY(embed_rmsnorm_launch(ids_dev, m->embed, c.vocab, m->layers[0].ln1, h, xn, R, H, eps, VX_F16, st));
+        VX_TRY(embed_rmsnorm_launch(ids_dev, ids_stride, m->embed, c.vocab, m->layers[0].ln1, h, xn, R, H, eps,
+                                    VX_F16, st));
     }
     int splits = 0;
     const float *part = nullptr;
@@ -931,7 +933,7 @@ struct vx_spec {
     int fix_hole;
     std::vector<SpecState> states;
     // device buffers for a round
-    DevBuf d_ids, d_cand, d_vids, d_tlog, d_dlog, d_acc, d_tok, d_uni, d_meta, d_argws, d_draw;
+    DevBuf d_res, d_vids, d_tlog, d_dlog, d_uni, d_meta, d_argws, d_draw;  // d_res: accepted | tokens | candidates
     DevBuf d_amax;  // greedy-argmax partials written by the LM heads: values then indices
     DevBuf d_plog;  // prefill-chunk logits (discarded, spec.rs:172-173)
     // host staging (pinned)
@@ -1225,14 +1227,11 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     VX_TRY(ensure_buffers(e->draft, n));
     VX_TRY(ensure_buffers(e->target, n * (D + 1)));
     VX_TRY(e->d_meta.ensure(total + small));
-    VX_TRY(e->d_ids.ensure(n * 4));
-    VX_TRY(e->d_cand.ensure(n * D * 4));
+    VX_TRY(e->d_res.ensure(res_bytes));
     VX_TRY(e->d_vids.ensure(n * (D + 1) * 4));
     VX_TRY(e->d_tlog.ensure((size_t)n * (D + 1) * V * 2));
     const bool stoch = temp > 0.f;
     VX_TRY(e->d_dlog.ensure((size_t)n * (stoch ? D : 1) * V * 2));
-    VX_TRY(e->d_acc.ensure(n * 4));
-    VX_TRY(e->d_tok.ensure(n * (D + 1) * 4));
     VX_TRY(e->d_uni.ensure(n * (D + 1) * 16));
     VX_TRY(e->d_draw.ensure(n * 4));
     const int64_t amax_chunks = vx_cdiv(V, 128);
@@ -1250,9 +1249,11 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     uint8_t *dm = (uint8_t *)e->d_meta.p;
     VX_HIP(hipMemcpyAsync(dm, hs, total + small, hipMemcpyHostToDevice, st));
     const uint32_t *d_last = (const uint32_t *)(dm + total);
-    uint32_t *cand = (uint32_t *)e->d_cand.p;
-    uint32_t *ids = (uint32_t *)e->d_ids.p;
-    VX_HIP(hipMemcpyAsync(ids, d_last, n * 4, hipMemcpyDeviceToDevice, st));
+    // the round's results in one buffer laid out like the host stage: accepted
+    // lengths [n], committed tokens [n, D+1], candidates [n, D]
+    int32_t *d_acc = (int32_t *)e->d_res.p;
+    uint32_t *d_tok = (uint32_t *)((uint8_t *)e->d_res.p + n * 4);
+    uint32_t *cand = d_tok + n * (D + 1);
     float *uni = (float *)e->d_uni.p;
     if (stoch) {
         hipLaunchKernelGGL(spec_uniforms_kernel, dim3((unsigned)vx_cdiv(n * (D + 1), 256)), dim3(256), 0, st, uni,
@@ -1278,8 +1279,11 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     for (int64_t i = 0; i < D; i++) {
         void *dl = stoch ? (void *)((uint16_t *)e->d_dlog.p + (size_t)i * n * V) : e->d_dlog.p;
         bool fused_amax = false;
-        VX_TRY(forward_dev(e->draft, e->dp, ids, metas[i], dm + boff[i], 0, dl, e->draft->ws.p, e->draft->ws.n, st,
-                           prof ? &e->prof_draft : nullptr, kv_draft, stoch ? nullptr : amax_v, amax_i, &fused_amax));
+        // step i's input: the last tokens, then column i - 1 of cand [n, D]
+        const uint32_t *in_ids = i == 0 ? d_last : cand + (i - 1);
+        VX_TRY(forward_dev(e->draft, e->dp, in_ids, metas[i], dm + boff[i], 0, dl, e->draft->ws.p, e->draft->ws.n,
+                           st, prof ? &e->prof_draft : nullptr, kv_draft, stoch ? nullptr : amax_v, amax_i,
+                           &fused_amax, i == 0 ? 1 : D));
         if (!stoch && fused_amax) {
             VX_TRY(argmax_accept_partials_launch(amax_v, amax_i, (int)amax_chunks, n, 0, 1, nullptr, 0, nullptr,
                                                  nullptr, cand + i, D, st));
@@ -1290,8 +1294,6 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
             VX_TRY(sample_rows_launch(dl, VX_BF16, uni + i * 4, (D + 1) * 4, (uint32_t *)e->d_draw.p, n, V,
                                       temp, cand + i, D, e->d_argws.p, e->d_argws.n, st));
         }
-        if (i + 1 < D)  // next draft input = column i of cand [n, D]
-            VX_HIP(hipMemcpy2DAsync(ids, 4, cand + i, D * 4, 4, n, hipMemcpyDeviceToDevice, st));
     }
     // ---- verify (spec.rs:246-264)
     hipLaunchKernelGGL(build_verify_ids, dim3((unsigned)vx_cdiv(n * (D + 1), 256)), dim3(256), 0, st, d_last, cand,
@@ -1306,15 +1308,15 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     // ---- acceptance (spec.rs:266-292)
     if (!stoch && verify_amax) {
         VX_TRY(argmax_accept_partials_launch(amax_v, amax_i, (int)amax_chunks, n * (D + 1), 1, (int)(D + 1), cand,
-                                             (int)D, (int32_t *)e->d_acc.p, (uint32_t *)e->d_tok.p, nullptr, 0, st));
+                                             (int)D, d_acc, d_tok, nullptr, 0, st));
     } else if (!stoch) {
         VX_TRY(argmax_accept_launch(e->d_tlog.p, VX_BF16, n * (D + 1), V, 1, (int)(D + 1), cand, (int)D,
-                                    (int32_t *)e->d_acc.p, (uint32_t *)e->d_tok.p, nullptr, nullptr, nullptr, nullptr,
+                                    d_acc, d_tok, nullptr, nullptr, nullptr, nullptr,
                                     0, e->d_argws.p, e->d_argws.n, st));
     } else {
         // draft logits are laid out [D][n][V] (step-major)
-        VX_TRY(stochastic_accept_launch(e->d_tlog.p, e->d_dlog.p, VX_BF16, cand, uni, (int32_t *)e->d_acc.p,
-                                        (uint32_t *)e->d_tok.p, n, D, V, temp, true, e->d_argws.p, e->d_argws.n,
+        VX_TRY(stochastic_accept_launch(e->d_tlog.p, e->d_dlog.p, VX_BF16, cand, uni, d_acc,
+                                        d_tok, n, D, V, temp, true, e->d_argws.p, e->d_argws.n,
                                         st));
     }
     // ---- results to host (one copy set, one sync)
@@ -1322,9 +1324,7 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     int32_t *h_acc = (int32_t *)hr;
     uint32_t *h_tok = (uint32_t *)(hr + n * 4);
     uint32_t *h_cand = h_tok + n * (D + 1);
-    VX_HIP(hipMemcpyAsync(h_acc, e->d_acc.p, n * 4, hipMemcpyDeviceToHost, st));
-    VX_HIP(hipMemcpyAsync(h_tok, e->d_tok.p, n * (D + 1) * 4, hipMemcpyDeviceToHost, st));
-    VX_HIP(hipMemcpyAsync(h_cand, cand, n * D * 4, hipMemcpyDeviceToHost, st));
+    VX_HIP(hipMemcpyAsync(hr, e->d_res.p, res_bytes, hipMemcpyDeviceToHost, st));
     if (prof) VX_HIP(hipEventRecord(e->ev[3], st));
     VX_HIP(hipStreamSynchronize(st));
     if (prof) {

@@ -56,19 +56,20 @@ __device__ __forceinline__ uint4 rms_apply8(const float (&x)[8], uint4 wv, float
 
 // y = round_bf16(x / sqrt(mean(x^2) + eps) * w) (candle RmsNorm in bf16), x, w
 // bf16, y as f16 carrier or bf16.  Rows optionally gathered through row_idx
-// (the last row per sequence, or token ids into the embedding table: indices
-// clamp to src_rows - 1), and the gathered rows optionally copied to xcopy
+// (the last row per sequence, or token ids into the embedding table, read
+// idx_stride apart: indices clamp to src_rows - 1), and the gathered rows
+// optionally copied to xcopy
 // (the embedding lookup, qwen3.rs:998, fused with the first layer's norm).
 // One workgroup per row, one thread per 8 columns; the row and the weights
 // are requested together up front.
 __global__ __launch_bounds__(1024) void rmsnorm_bf16_kernel(const uint16_t *x, const uint16_t *w, uint16_t *y,
                                                            const uint32_t *row_idx, int H, float eps, int out_dt,
-                                                           int64_t src_rows, uint16_t *xcopy) {
+                                                           int64_t src_rows, uint16_t *xcopy, int64_t idx_stride) {
     __shared__ float red[16];
     const int r = blockIdx.x;
     const int i = threadIdx.x;
     const bool live = i < H / 8;
-    const int64_t src_r = row_idx ? std::min<int64_t>(row_idx[r], src_rows - 1) : r;
+    const int64_t src_r = row_idx ? std::min<int64_t>(row_idx[(int64_t)r * idx_stride], src_rows - 1) : r;
     const uint4 xv = live ? ((const uint4 *)(x + src_r * H))[i] : make_uint4(0u, 0u, 0u, 0u);
     if (xcopy && live) ((uint4 *)(xcopy + (int64_t)r * H))[i] = xv;
     const uint4 wv = live ? ((const uint4 *)w)[i] : make_uint4(0u, 0u, 0u, 0u);
@@ -921,21 +922,22 @@ int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint
     if (rows == 0) return 0;
     const unsigned threads = (unsigned)vx_cdiv(H / 8, 64) * 64;
     hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(threads), 0, st, x, w, y, row_idx, (int)H,
-                       eps, out_dt, INT64_MAX, (uint16_t *)nullptr);
+                       eps, out_dt, INT64_MAX, (uint16_t *)nullptr, (int64_t)1);
     VX_HIP(hipGetLastError());
     return 0;
 }
 
-// Embedding lookup fused with the first layer's norm: h[r] = embed[ids[r]]
-// (ids clamped to the vocabulary) and y[r] = RMSNorm(h[r]) * w.
-int embed_rmsnorm_launch(const uint32_t *ids, const uint16_t *embed, int64_t vocab, const uint16_t *w,
-                         uint16_t *h, uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt, hipStream_t st) {
+// Embedding lookup fused with the first layer's norm: h[r] = embed[ids[r *
+// ids_stride]] (ids clamped to the vocabulary) and y[r] = RMSNorm(h[r]) * w.
+int embed_rmsnorm_launch(const uint32_t *ids, int64_t ids_stride, const uint16_t *embed, int64_t vocab,
+                         const uint16_t *w, uint16_t *h, uint16_t *y, int64_t rows, int64_t H, float eps, int out_dt,
+                         hipStream_t st) {
     if (H % 8 != 0 || H > 8 * 1024) return set_error("rmsnorm: hidden size must be a multiple of 8 and <= 8192");
     if (vocab < 1) return set_error("embedding: empty vocabulary");
     if (rows == 0) return 0;
     const unsigned threads = (unsigned)vx_cdiv(H / 8, 64) * 64;
     hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(threads), 0, st, embed, w, y, ids, (int)H,
-                       eps, out_dt, vocab, h);
+                       eps, out_dt, vocab, h, ids_stride);
     VX_HIP(hipGetLastError());
     return 0;
 }
