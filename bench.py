@@ -34,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_MFMA_F16_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
 METRIC = "accepted tok/s, Qwen3-4B-shape int4 k=4 batch 16; verify-step HBM GB/s"
 # HBM bytes per verify GEMM op measured with rocprofv3 --pmc FETCH_SIZE /
 # WRITE_SIZE over this bench, scaled by a calibration copy (see the file)
@@ -165,6 +166,12 @@ def run_spec(args):
         agg, qmm_gbs, verify_bytes, verify_gbs = None, None, None, None
     # the measured device copy rate, reported next to the published peak
     copy_gbs = device_copy_gbs() if profs else None
+    # the same GEMM ops against the dense f16 MFMA peak: algorithmic flops
+    # (2 M N K over the verify rows M = B (k+1), no padding) per round
+    H, F, V, L = cfg["hidden"], cfg["inter"], cfg["vocab"], cfg["layers"]
+    QW, KW = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    verify_flops = 2.0 * B * (k + 1) * (L * (H * (QW + 2 * KW) + QW * H + H * 2 * F + F * H) + H * V)
+    qmm_tflops = None if agg is None else verify_flops / (agg["verify_qmm_ms"] * 1e-3) / 1e12
     res = {
         "metric": METRIC,
         "value": committed / elapsed,
@@ -191,6 +198,8 @@ def run_spec(args):
                      "achieved": qmm_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": None if qmm_gbs is None else qmm_gbs / PEAK_HBM_GBS,
                      "device_copy_gbs": copy_gbs,
+                     "mfma_tflops": qmm_tflops, "mfma_peak_tflops": PEAK_MFMA_F16_TFLOPS,
+                     "mfma_frac": None if qmm_tflops is None else qmm_tflops / PEAK_MFMA_F16_TFLOPS,
                      "traffic": traffic_per_op(),
                      "launches_per_step": None if agg is None else agg["verify_qmm_launches"],
                      "avg_launch_us": None if agg is None else
