@@ -107,7 +107,10 @@ constexpr size_t attn_lds_bytes() {
     return vt > comb ? vt : comb;
 }
 
-template <int KT, int D, int QT>
+// FUSE: the instantiation that finishes q/k/v from the qkv partials (a.qkv);
+// the plain one compiles without that prologue, whose register arrays would
+// otherwise set the register allocation (and occupancy) of every launch.
+template <int KT, int D, int QT, bool FUSE>
 __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     typedef typename MfmaT<KT>::frag frag;
     constexpr int DK = D / 32;  // MFMA k-steps over head_dim
@@ -155,7 +158,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     // split's new K/V rows into the pools.  One wave per vector; a wave takes
     // its vectors kVB at a time and requests every split partial of the
     // batch before summing, so a batch costs one memory round trip.
-    if (a.qkv) {
+    if constexpr (FUSE) {
         constexpr int kVB = 8;
         constexpr int kPairs = (D / 2 + 63) / 64;  // RoPE pairs per lane
         constexpr int kE = 2 * kPairs;             // elements per lane and vector
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < DK; ks++) {
             uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-            if (a.qkv)
+            if constexpr (FUSE)
                 raw = *(const uint4 *)((const uint16_t *)smem + n * D + ks * 32 + lg * 8);
             else if (live)
                 raw = *(const uint4 *)((const uint16_t *)a.q + ((int64_t)(row0 + t) * a.h_q + hq) * D + ks * 32 + lg * 8);
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
         }
     }
     // qbuf shares LDS with the V^T tiles of the key loop
-    if (a.qkv) __syncthreads();
+    if constexpr (FUSE) __syncthreads();
 
     floatx4 o[DT][QT];
 #pragma unroll
@@ -624,7 +627,12 @@ __global__ void zero_u16_kernel(uint16_t *p, int64_t n) {
 
 template <int KT, int D, int QT>
 void launch_attn(const AttnArgs &a, int64_t n_items, hipStream_t st) {
-    hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT>), dim3((unsigned)n_items), dim3(64 * kAttnWaves), 0, st, a);
+    if (a.qkv)
+        hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT, true>), dim3((unsigned)n_items), dim3(64 * kAttnWaves), 0,
+                           st, a);
+    else
+        hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT, false>), dim3((unsigned)n_items), dim3(64 * kAttnWaves), 0,
+                           st, a);
 }
 
 template <int KT>
