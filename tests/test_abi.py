@@ -79,3 +79,27 @@ def test_no_fallback_when_library_missing(tmp_path, monkeypatch):
     mod = importlib.util.module_from_spec(spec)
     with pytest.raises(ImportError, match="no CPU fallback"):
         spec.loader.exec_module(mod)
+
+
+def test_empty_inputs_are_no_ops():
+    """Zero rows are valid input to every kernel entry point (the reference
+    returns empty tensors): the call succeeds without touching the pointers,
+    which PyTorch leaves null for zero-element tensors.  Shape validation
+    still runs first."""
+    L, F16, BF16 = _lib.lib, _lib.F16, _lib.BF16
+    Z = None
+    assert L.vx_qmm_4bit(Z, Z, Z, Z, Z, Z, 0, 4096, 256, 64, F16, Z) == 0
+    assert L.vx_qmm_4bit(Z, Z, Z, Z, Z, Z, 5, 0, 256, 64, F16, Z) == 0
+    assert "multiple of 8" in _err(L.vx_qmm_4bit(Z, Z, Z, Z, Z, Z, 0, 4096, 12, 64, F16, Z))
+    assert L.vx_qmm_4bit_ex(Z, Z, Z, Z, Z, Z, 0, 128, 256, 64, 0, BF16, F16, _lib.EPI_STORE, Z, 0, Z) == 0
+    assert L.vx_qmm_4bit_packed(Z, Z, Z, Z, 0, 128, 256, 0, BF16, F16, _lib.EPI_STORE, Z, 0, Z) == 0
+    assert L.vx_paged_attention(Z, Z, Z, Z, Z, Z, Z, Z, Z, 0, 0, 1, 1, 4, 2, 64, 16, 0.125, 0, F16, Z) == 0
+    assert "divisible" in _err(L.vx_paged_attention(Z, Z, Z, Z, Z, Z, Z, Z, Z, 0, 0, 1, 1, 4, 3, 64, 16, 0.125,
+                                                    0, F16, Z))
+    assert L.vx_paged_decode_attention(Z, Z, Z, Z, Z, Z, 0, 1, 1, 4, 2, 64, 16, 0.125, 0, F16, Z) == 0
+    assert L.vx_rope_inplace(Z, Z, Z, Z, 0, 4, 64, 16, BF16, Z) == 0
+    assert L.vx_kv_scatter(Z, Z, Z, Z, 0, 1, 2, 16, 64, F16, Z) == 0
+    assert L.vx_argmax_rows(Z, Z, 0, 10, BF16, Z) == 0
+    assert L.vx_accept_greedy(Z, Z, Z, Z, 0, 4, 10, BF16, Z) == 0
+    assert L.vx_accept_stochastic(Z, Z, Z, Z, Z, Z, 0, 4, 10, 0.8, BF16, Z, 0, Z) == 0
+    assert L.vx_sample_rows(Z, Z, 1, Z, 0, 10, 0.8, BF16, Z, 0, Z) == 0

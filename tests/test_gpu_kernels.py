@@ -659,3 +659,31 @@ def test_kv_compact_path(cuda):
         _pool_copy(got.data_ptr(), pg.layer_pool_ptr(i // 2, i % 2), pool_elems * 2)
         torch.cuda.synchronize()
         assert np.array_equal(got.cpu().numpy().reshape(P, HK, ps, D), want), f"pool {i} differs"
+
+
+def test_empty_batches_through_the_drop_ins(cuda):
+    """Zero rows through the reference-shaped operators return empty results
+    (torch hands zero-element tensors over with null data pointers)."""
+    from velox_amd import ops
+
+    lin = synth_linear(256, 256, 3)
+    y = ops.qmm_4bit(torch.empty((0, 256), dtype=torch.float16, device="cuda"), u32(lin["qweight"]),
+                     dev(lin["scales"]), dev(lin["biases"]), None, 64)
+    assert tuple(y.shape) == (0, 256)
+    kp = torch.zeros((4, 2, 16, 64), dtype=torch.float16, device="cuda")
+    u = lambda *s: torch.zeros(s, dtype=torch.int32, device="cuda")  # noqa: E731
+    out = ops.paged_prefill_attention(torch.empty((0, 4, 64), dtype=torch.float16, device="cuda"), kp, kp.clone(),
+                                      u(0, 2), u(1), u(0), u(0), 0.125)
+    assert tuple(out.shape) == (0, 4, 64)
+    out = ops.paged_decode_attention(torch.empty((0, 4, 64), dtype=torch.float16, device="cuda"), kp, kp.clone(),
+                                     u(0, 2), u(0), 0.125)
+    assert tuple(out.shape) == (0, 4, 64)
+    tab = torch.zeros((16, 32), dtype=torch.bfloat16, device="cuda")
+    ops.batched_rope_decode(torch.empty((0, 4, 64), dtype=torch.bfloat16, device="cuda"), tab, tab.clone(), u(0))
+    before = kp.clone()
+    ops.batched_scatter(kp, torch.empty((0, 2, 64), dtype=torch.float16, device="cuda"), u(0), u(0))
+    assert torch.equal(kp, before)
+    assert tuple(ops.argmax_rows(torch.empty((0, 10), dtype=torch.bfloat16, device="cuda")).shape) == (0,)
+    acc, tok = ops.accept_greedy(torch.empty((0, 5, 10), dtype=torch.bfloat16, device="cuda"), u(0, 4))
+    assert tuple(acc.shape) == (0,) and tuple(tok.shape) == (0, 5)
+    torch.cuda.synchronize()

@@ -787,6 +787,7 @@ extern "C" int vx_paged_attention(const void *q, const void *k_pool, const void 
                                   int64_t h_q, int64_t h_kv, int64_t head_dim, int64_t page_size,
                                   float scale, uint32_t sliding_window, int dtype, void *stream) {
     VX_TRY(check_attn_shapes(h_q, h_kv, head_dim, dtype));
+    if (total_q == 0 || n_seqs == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(q && k_pool && v_pool && block_table && cu_seqlens && kv_offsets && out,
                "paged_attention: null tensor");
     VX_REQUIRE(max_blocks > 0 && num_pages > 0 && page_size > 0, "paged_attention: empty pool");
@@ -805,6 +806,7 @@ extern "C" int vx_paged_decode_attention(const void *q, const void *k_pool, cons
                                          int64_t page_size, float scale, uint32_t sliding_window,
                                          int dtype, void *stream) {
     VX_TRY(check_attn_shapes(h_q, h_kv, head_dim, dtype));
+    if (n == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(q && k_pool && v_pool && block_table && kv_lens && out, "paged_decode_attention: null tensor");
     VX_REQUIRE(max_blocks > 0 && num_pages > 0 && page_size > 0, "paged_decode_attention: empty pool");
     return paged_attention_launch(q, k_pool, v_pool, block_table, nullptr, kv_lens, nullptr, out, 1, n, n,

@@ -996,11 +996,10 @@ extern "C" int vx_rope_inplace(void *x, const void *cos_t, const void *sin_t, co
                                int64_t n, int64_t h, int64_t d, int64_t max_pos, int dtype,
                                void *stream) {
     VX_REQUIRE(d % 2 == 0, "batched_rope_decode: D must be even");
-    VX_REQUIRE(x && cos_t && sin_t && offsets, "batched_rope_decode: null tensor");
     VX_REQUIRE(max_pos > 0, "batched_rope_decode: empty tables");
-    (void)max_pos;
     const int64_t tot = n * h * (d / 2);
-    if (tot == 0) return 0;
+    if (tot == 0) return 0;  // empty tensors may carry null data pointers
+    VX_REQUIRE(x && cos_t && sin_t && offsets, "batched_rope_decode: null tensor");
     hipStream_t st = (hipStream_t)stream;
     dim3 grid((unsigned)vx_cdiv(tot, 256));
     if (dtype == VX_F32)
@@ -1018,11 +1017,11 @@ extern "C" int vx_rope_inplace(void *x, const void *cos_t, const void *sin_t, co
 extern "C" int vx_kv_scatter(void *pool, const void *values, const uint32_t *page_ids,
                              const uint32_t *slots, int64_t n, int64_t num_pages, int64_t h,
                              int64_t page_size, int64_t d, int dtype, void *stream) {
-    VX_REQUIRE(pool && values && page_ids && slots, "batched_scatter: null tensor");
     VX_REQUIRE(dtype == VX_F32 || dtype == VX_F16 || dtype == VX_BF16, "batched_scatter: unsupported dtype");
     const int64_t esz = dtype == VX_F32 ? 4 : 2;
     VX_REQUIRE((d * esz) % 4 == 0, "batched_scatter: row bytes must be a multiple of 4");
-    if (n == 0 || h == 0) return 0;
+    if (n == 0 || h == 0) return 0;  // empty tensors may carry null data pointers
+    VX_REQUIRE(pool && values && page_ids && slots, "batched_scatter: null tensor");
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)(n * h)), dim3(64), 0, st, (uint8_t *)pool,
                        (const uint8_t *)values, page_ids, slots, n, h, page_size, d * esz, num_pages);
@@ -1032,8 +1031,8 @@ extern "C" int vx_kv_scatter(void *pool, const void *values, const uint32_t *pag
 
 extern "C" int vx_argmax_rows(const void *logits, uint32_t *out, int64_t rows, int64_t vocab,
                               int logits_dtype, void *stream) {
+    if (rows == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(logits && out, "argmax: null tensor");
-    if (rows == 0) return 0;
     return argmax_accept_launch(logits, logits_dtype, rows, vocab, 0, 1, nullptr, 0, nullptr, nullptr,
                                 nullptr, nullptr, out, nullptr, 0, nullptr, 0, (hipStream_t)stream);
 }
@@ -1042,9 +1041,9 @@ extern "C" int vx_accept_greedy(const void *logits, const uint32_t *candidates, 
                                 uint32_t *tokens, int64_t batch, int64_t k, int64_t vocab,
                                 int logits_dtype, void *stream) {
     VX_REQUIRE(k >= 1, "draft_k must be >= 1");
-    VX_REQUIRE(logits && candidates && accepted && tokens, "accept_greedy: null tensor");
     VX_REQUIRE(k + 1 <= 64, "accept_greedy: k too large");
-    if (batch == 0) return 0;
+    if (batch == 0) return 0;  // empty tensors may carry null data pointers
+    VX_REQUIRE(logits && candidates && accepted && tokens, "accept_greedy: null tensor");
     return argmax_accept_launch(logits, logits_dtype, batch * (k + 1), vocab, 1, (int)(k + 1), candidates,
                                 (int)k, accepted, tokens, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
                                 0, (hipStream_t)stream);
@@ -1067,9 +1066,9 @@ extern "C" int vx_accept_stochastic(const void *target_logits, const void *draft
                                     uint32_t *tokens, int64_t batch, int64_t k, int64_t vocab,
                                     float temperature, int logits_dtype, void *workspace,
                                     size_t workspace_bytes, void *stream) {
+    if (batch == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(target_logits && draft_logits && candidates && uniforms && accepted && tokens,
                "accept_stochastic: null tensor");
-    if (batch == 0) return 0;
     return stochastic_accept_launch(target_logits, draft_logits, logits_dtype, candidates, uniforms, accepted,
                                     tokens, batch, k, vocab, temperature, false, workspace, workspace_bytes,
                                     (hipStream_t)stream);
@@ -1078,8 +1077,8 @@ extern "C" int vx_accept_stochastic(const void *target_logits, const void *draft
 extern "C" int vx_sample_rows(const void *logits, const float *uniforms, int64_t uniform_stride,
                               uint32_t *out, int64_t rows, int64_t vocab, float temperature,
                               int logits_dtype, void *workspace, size_t workspace_bytes, void *stream) {
+    if (rows == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(logits && uniforms && out, "sample: null tensor");
-    if (rows == 0) return 0;
     return sample_rows_launch(logits, logits_dtype, uniforms, uniform_stride, out, rows, vocab, temperature,
                               nullptr, 0, workspace, workspace_bytes, (hipStream_t)stream);
 }

@@ -1889,9 +1889,9 @@ extern "C" int vx_qmm_pack_4bit(const uint32_t *qweight, const void *scales, con
 extern "C" int vx_qmm_4bit_packed(const void *x, const void *packed, void *y, const void *residual, int64_t m,
                                   int64_t n, int64_t k, int x_shift, int round_dtype, int y_dtype, int epilogue,
                                   void *workspace, size_t workspace_bytes, void *stream) {
+    if (m == 0 || n == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(x && packed && y, "qmm_4bit_packed: null tensor");
     VX_REQUIRE(epilogue != VX_EPI_RESIDUAL || residual, "qmm_4bit_packed: residual epilogue needs R");
-    if (m == 0 || n == 0) return 0;
     return qmm_packed(x, packed, y, residual, m, n, k, x_shift, 0, round_dtype, y_dtype, epilogue, workspace,
                       workspace_bytes, (hipStream_t)stream);
 }
@@ -1905,8 +1905,8 @@ extern "C" int vx_qmm_4bit(const void *x, const uint32_t *qweight, const void *s
                "qmm_4bit: group_size must be a multiple of 8 and divide K");
     VX_REQUIRE(dtype == VX_F32 || dtype == VX_F16 || dtype == VX_BF16, "qmm_4bit: unsupported dtype");
     VX_REQUIRE(m >= 0 && n >= 0, "qmm_4bit: negative shape");
+    if (m == 0 || n == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(x && qweight && scales && biases && y, "qmm_4bit: null tensor");
-    if (m == 0 || n == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     if (dtype != VX_F32 && fast_ok(dtype, k, group_size, x, qweight, scales, biases) && m * n < ((int64_t)1 << 31)) {
         VX_TRY(qmm_fast(x, qweight, scales, biases, y, nullptr, m, n, k, dtype, 0, dtype, dtype,
@@ -1940,10 +1940,10 @@ extern "C" int vx_qmm_4bit_ex(const void *x, const uint32_t *qweight, const void
                               size_t workspace_bytes, void *stream) {
     VX_REQUIRE(group_size == 64, "qmm_4bit_ex: group_size must be 64");
     VX_REQUIRE(k % 128 == 0, "qmm_4bit_ex: K must be a multiple of 128");
+    if (m == 0 || n == 0) return 0;  // empty tensors may carry null data pointers
     VX_REQUIRE(x && qweight && scales && biases && y, "qmm_4bit_ex: null tensor");
     VX_REQUIRE(epilogue != VX_EPI_RESIDUAL || residual, "qmm_4bit_ex: residual epilogue needs R");
     VX_REQUIRE(fast_ok(VX_F16, k, group_size, x, qweight, scales, biases), "qmm_4bit_ex: misaligned operand");
-    if (m == 0 || n == 0) return 0;
     return qmm_fast(x, qweight, scales, biases, y, residual, m, n, k, VX_F16, x_shift, round_dtype,
                     y_dtype, epilogue, workspace, workspace_bytes, (hipStream_t)stream);
 }
