@@ -241,51 +241,78 @@ int vxo_paged_attention(const float *q, const float *k_pool, const float *v_pool
                         uint32_t sliding_window, float *out) {
     if (h_kv <= 0 || h_q % h_kv != 0) return set_err("attention: H_q must be divisible by H_kv");
     const int64_t groups = h_q / h_kv;
-    float *acc = (float *)malloc(sizeof(float) * (size_t)d);
-    if (!acc) return set_err("attention: oom");
+    /* block-table bounds first (same visiting rule as the main loop), so the
+     * rows can then run in parallel: each output element keeps the serial
+     * per-row online-softmax order of paged_decode_attention_cpu */
     for (int64_t row = 0; row < total_q; row++) {
         int64_t seq = 0;
         while (seq + 1 < n_seqs && (int64_t)cu_seqlens[seq + 1] <= row) seq++;
         const int64_t t = row - cu_seqlens[seq];
         const int64_t off = kv_offsets[seq];
         const int64_t r_seq = (int64_t)cu_seqlens[seq + 1] - (int64_t)cu_seqlens[seq];
-        /* last visible position + 1 */
         const int64_t end = tree_mask ? off + r_seq : off + t + 1;
         const int64_t self_len = off + t + 1;
         const int64_t w = sliding_window;
         const int64_t start = (w > 0 && self_len > w) ? self_len - w : 0;
-        for (int64_t hq = 0; hq < h_q; hq++) {
-            const int64_t hk = hq / groups;
-            float m = -INFINITY, l = 0.0f;
-            for (int64_t i = 0; i < d; i++) acc[i] = 0.0f;
-            const float *qr = q + (row * h_q + hq) * d;
-            for (int64_t pos = start; pos < end; pos++) {
-                if (tree_mask && pos >= off) {
-                    const int64_t j = pos - off;
-                    if (j >= 64 || !((tree_mask[row] >> j) & 1ull)) continue;
-                }
-                const int64_t blk = pos / ps;
-                if (blk >= max_blocks) {
-                    free(acc);
-                    return set_err("attention: block_table too short");
-                }
-                const int64_t page = block_table[seq * max_blocks + blk];
-                const int64_t base = page * (h_kv * ps * d) + hk * (ps * d) + (pos % ps) * d;
-                float s = 0.0f;
-                for (int64_t i = 0; i < d; i++) s += qr[i] * k_pool[base + i];
-                s *= scale;
-                const float new_m = fmaxf(m, s);
-                const float alpha = expf(m - new_m);
-                const float beta = expf(s - new_m);
-                for (int64_t i = 0; i < d; i++) acc[i] = acc[i] * alpha + beta * v_pool[base + i];
-                l = l * alpha + beta;
-                m = new_m;
+        for (int64_t pos = start; pos < end; pos++) {
+            if (tree_mask && pos >= off) {
+                const int64_t j = pos - off;
+                if (j >= 64 || !((tree_mask[row] >> j) & 1ull)) continue;
             }
-            float *o = out + (row * h_q + hq) * d;
-            for (int64_t i = 0; i < d; i++) o[i] = acc[i] / l;
+            if (pos / ps >= max_blocks) return set_err("attention: block_table too short");
         }
     }
-    free(acc);
+    int oom = 0;
+#pragma omp parallel
+    {
+        float *acc = (float *)malloc(sizeof(float) * (size_t)d);
+        if (!acc) {
+#pragma omp atomic write
+            oom = 1;
+        }
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t row = 0; row < total_q; row++) {
+            if (!acc) continue;
+            int64_t seq = 0;
+            while (seq + 1 < n_seqs && (int64_t)cu_seqlens[seq + 1] <= row) seq++;
+            const int64_t t = row - cu_seqlens[seq];
+            const int64_t off = kv_offsets[seq];
+            const int64_t r_seq = (int64_t)cu_seqlens[seq + 1] - (int64_t)cu_seqlens[seq];
+            /* last visible position + 1 */
+            const int64_t end = tree_mask ? off + r_seq : off + t + 1;
+            const int64_t self_len = off + t + 1;
+            const int64_t w = sliding_window;
+            const int64_t start = (w > 0 && self_len > w) ? self_len - w : 0;
+            for (int64_t hq = 0; hq < h_q; hq++) {
+                const int64_t hk = hq / groups;
+                float m = -INFINITY, l = 0.0f;
+                for (int64_t i = 0; i < d; i++) acc[i] = 0.0f;
+                const float *qr = q + (row * h_q + hq) * d;
+                for (int64_t pos = start; pos < end; pos++) {
+                    if (tree_mask && pos >= off) {
+                        const int64_t j = pos - off;
+                        if (j >= 64 || !((tree_mask[row] >> j) & 1ull)) continue;
+                    }
+                    const int64_t blk = pos / ps;
+                    const int64_t page = block_table[seq * max_blocks + blk];
+                    const int64_t base = page * (h_kv * ps * d) + hk * (ps * d) + (pos % ps) * d;
+                    float s = 0.0f;
+                    for (int64_t i = 0; i < d; i++) s += qr[i] * k_pool[base + i];
+                    s *= scale;
+                    const float new_m = fmaxf(m, s);
+                    const float alpha = expf(m - new_m);
+                    const float beta = expf(s - new_m);
+                    for (int64_t i = 0; i < d; i++) acc[i] = acc[i] * alpha + beta * v_pool[base + i];
+                    l = l * alpha + beta;
+                    m = new_m;
+                }
+                float *o = out + (row * h_q + hq) * d;
+                for (int64_t i = 0; i < d; i++) o[i] = acc[i] / l;
+            }
+        }
+        free(acc);
+    }
+    if (oom) return set_err("attention: oom");
     return 0;
 }
 
@@ -386,9 +413,12 @@ void vxo_row_softmax_stats(const float *row, int64_t vocab, float inv_t, float *
         const int64_t hi = lo + VXO_SM_CHUNK < vocab ? lo + VXO_SM_CHUNK : vocab;
         float m = -INFINITY;
         for (int64_t j = lo; j < hi; j++) m = fmaxf(m, row[j]);
+        /* a chunk with no finite maximum holds no probability mass (its
+         * (row[j] - m) would be -inf - -inf) */
         for (int t = 0; t < VXO_SM_THREADS; t++) {
             float s = 0.0f;
-            for (int64_t j = lo + t; j < hi; j += VXO_SM_THREADS) s = s + vxo_expf((row[j] - m) * inv_t);
+            if (m != -INFINITY)
+                for (int64_t j = lo + t; j < hi; j += VXO_SM_THREADS) s = s + vxo_expf((row[j] - m) * inv_t);
             part[t] = s;
         }
         mc[c] = m;
@@ -397,7 +427,8 @@ void vxo_row_softmax_stats(const float *row, int64_t vocab, float inv_t, float *
     float M = -INFINITY;
     for (int64_t c = 0; c < nch; c++) M = fmaxf(M, mc[c]);
     float Z = 0.0f;
-    for (int64_t c = 0; c < nch; c++) Z = Z + zc[c] * vxo_expf((mc[c] - M) * inv_t);
+    for (int64_t c = 0; c < nch; c++)
+        if (mc[c] != -INFINITY) Z = Z + zc[c] * vxo_expf((mc[c] - M) * inv_t);
     *m_out = M;
     *z_out = Z;
     free(mc);
@@ -406,9 +437,10 @@ void vxo_row_softmax_stats(const float *row, int64_t vocab, float inv_t, float *
 
 static float resid_elem(const float *lt, float mt, float zt, const float *ld, float md, float zd,
                         float inv_t, int64_t j) {
-    const float p = vxo_expf((lt[j] - mt) * inv_t) / zt;
+    /* a row with no finite logit has no mass anywhere */
+    const float p = mt == -INFINITY ? 0.0f : vxo_expf((lt[j] - mt) * inv_t) / zt;
     if (!ld) return p;
-    const float q = vxo_expf((ld[j] - md) * inv_t) / zd;
+    const float q = md == -INFINITY ? 0.0f : vxo_expf((ld[j] - md) * inv_t) / zd;
     const float d = p - q;
     return d > 0.0f ? d : 0.0f;
 }
@@ -492,7 +524,7 @@ uint32_t vxo_sample_residual(const float *lt, float mt, float zt, const float *l
 }
 
 static float prob_of(const float *row, float m, float z, float inv_t, uint32_t tok) {
-    return vxo_expf((row[tok] - m) * inv_t) / z;
+    return m == -INFINITY ? 0.0f : vxo_expf((row[tok] - m) * inv_t) / z;
 }
 
 void vxo_sample_draft(const float *draft_logits, const float *uniforms, int64_t batch, int64_t k,

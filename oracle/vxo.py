@@ -52,6 +52,8 @@ def _load() -> C.CDLL:
         "vxo_argmax": (C.c_uint32, [_f32p, _i64]),
         "vxo_accept_greedy": (None, [_f32p, _i64, _u32p, _i64, _i64, _i32p, _u32p]),
         "vxo_row_softmax_stats": (None, [_f32p, _i64, C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+        "vxo_sample_residual": (C.c_uint32, [_f32p, C.c_float, C.c_float, vp, C.c_float, C.c_float, _i64,
+                                             C.c_float, C.c_float]),
         "vxo_sample_draft": (None, [_f32p, _f32p, _i64, _i64, _i64, C.c_float, _u32p]),
         "vxo_accept_stochastic": (None, [_f32p, _f32p, _u32p, _f32p, _i64, _i64, _i64, C.c_float, _i32p, _u32p]),
         "vxo_accept_tree": (None, [_f32p, _i32p, _u32p, _i64, _i64, _i64, _i32p, _i32p, _u32p]),
@@ -213,6 +215,17 @@ def row_softmax_stats(row, inv_t):
     m, z = C.c_float(), C.c_float()
     lib.vxo_row_softmax_stats(row, row.size, inv_t, C.byref(m), C.byref(z))
     return m.value, z.value
+
+
+def sample_residual(lt, mt, zt, u, inv_t, ld=None, md=0.0, zd=1.0) -> int:
+    """Inverse-CDF draw from max(0, p - q) (q absent: from p) with the
+    statistics (m, z) of each row, as the acceptance kernels use it."""
+    lt = np.ascontiguousarray(lt, np.float32)
+    ldp = None
+    if ld is not None:
+        ld = np.ascontiguousarray(ld, np.float32)
+        ldp = ld.ctypes.data
+    return int(lib.vxo_sample_residual(lt, mt, zt, ldp, md, zd, lt.size, inv_t, u))
 
 
 def sample_draft(draft_logits, uniforms, inv_t):

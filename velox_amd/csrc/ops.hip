@@ -430,8 +430,11 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const void *logits, 
     }
     m = red[0];
     __syncthreads();
+    // a chunk with no finite maximum holds no probability mass
     float s = 0.f;
-    for (int64_t j = lo + threadIdx.x; j < hi; j += 256) s = __fadd_rn(s, vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(r, j), m), inv_t)));
+    if (m != -__builtin_inff())
+        for (int64_t j = lo + threadIdx.x; j < hi; j += 256)
+            s = __fadd_rn(s, vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(r, j), m), inv_t)));
     red[threadIdx.x] = s;
     __syncthreads();
     for (int st = 128; st > 0; st >>= 1) {
@@ -450,15 +453,16 @@ __device__ __forceinline__ void combine_stats(const float *cm, const float *cz, 
     for (int c = 0; c < n_chunks; c++) M = fmaxf(M, cm[c]);
     Z = 0.f;
     for (int c = 0; c < n_chunks; c++)
-        Z = __fadd_rn(Z, __fmul_rn(cz[c], vx_detexp(__fmul_rn(__fsub_rn(cm[c], M), inv_t))));
+        if (cm[c] != -__builtin_inff()) Z = __fadd_rn(Z, __fmul_rn(cz[c], vx_detexp(__fmul_rn(__fsub_rn(cm[c], M), inv_t))));
 }
 
 template <int DT>
 __device__ __forceinline__ float resid_elem(const void *lt, float mt, float zt, const void *ld,
                                             float md, float zd, float inv_t, int64_t j) {
-    const float p = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(lt, j), mt), inv_t)), zt);
+    // a row with no finite logit has no mass anywhere
+    const float p = mt == -__builtin_inff() ? 0.f : __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(lt, j), mt), inv_t)), zt);
     if (!ld) return p;
-    const float q = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(ld, j), md), inv_t)), zd);
+    const float q = md == -__builtin_inff() ? 0.f : __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_elem<DT>(ld, j), md), inv_t)), zd);
     const float d = __fsub_rn(p, q);
     return d > 0.f ? d : 0.f;
 }
@@ -695,8 +699,8 @@ __global__ __launch_bounds__(64) void stochastic_walk_kernel(
             lt_c = ld_elem<VX_F32>(tr, c);
             ld_c = ld_elem<VX_F32>(dr, c);
         }
-        const float p = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(lt_c, mt), inv_t)), zt);
-        const float q = __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_c, md), inv_t)), zd);
+        const float p = mt == -__builtin_inff() ? 0.f : __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(lt_c, mt), inv_t)), zt);
+        const float q = md == -__builtin_inff() ? 0.f : __fdiv_rn(vx_detexp(__fmul_rn(__fsub_rn(ld_c, md), inv_t)), zd);
         const float ratio = __fdiv_rn(p, q);
         const float acc = ratio < 1.0f ? ratio : 1.0f;
         if (!(uni[trow * 4 + 1] < acc)) {
