@@ -289,6 +289,27 @@ int vx_spec_state_tokens(const vx_spec *e, int64_t state, uint32_t *out, int64_t
  * logits [n, k+1, vocab] as f32. */
 int vx_spec_last_trace(const vx_spec *e, uint32_t *candidates, float *verify_logits);
 
+/* Round trace (no reference counterpart: the reference's spec test reads
+ * only committed tokens, tests/spec_decode.rs:182-213).  It lets a checker
+ * re-derive every decision of the last vx_spec_step from the GPU's own
+ * inputs.  With tracing enabled, greedy rounds keep the logits of every draft
+ * step (stochastic rounds always do); it costs n * k * vocab * 2 bytes. */
+typedef struct {
+    int64_t n, draft_k, vocab;
+    float temperature;          /* of the last round; 0 = greedy */
+    int32_t has_draft_logits;   /* draft logits of every step are available */
+    uint64_t serial;            /* number of rounds run by the engine (0: none) */
+} vx_round_trace;
+int vx_spec_set_tracing(vx_spec *e, int enable);
+/* state_ids [n], stream_ids [n], rounds [n] (the Philox counter words the
+ * round's uniforms were drawn with); each may be NULL. */
+int vx_spec_last_trace_info(const vx_spec *e, vx_round_trace *info, int64_t *state_ids,
+                            uint32_t *stream_ids, uint32_t *rounds);
+/* draft_logits [n, k, vocab] as f32 (sequence-major; the values the draft
+ * argmax or draw read), uniforms [n, k+1, 4] (zeros for a greedy round);
+ * each may be NULL. */
+int vx_spec_last_trace_draft(const vx_spec *e, float *draft_logits, float *uniforms);
+
 /* Per-kernel HIP-event timing of a step (no reference counterpart: the
  * reference's only timing is Instant around calls, tests/spec_decode.rs).
  * Classes: 0 = int4 GEMM, 1 = paged attention, 2 = other.  Bytes are

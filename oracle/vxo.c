@@ -207,26 +207,49 @@ int vxo_qmm_4bit(const float *x, const uint32_t *qweight, const float *scales,
     if (gs == 0 || gs % 8 != 0 || k % gs != 0)
         return set_err("qmm_4bit: group_size must be a multiple of 8 and divide K");
     const int64_t k_packed = k / 8, k_groups = k / gs;
-    memset(out, 0, sizeof(float) * (size_t)(m * n));
     if (threads < 1) threads = 1;
-#pragma omp parallel for schedule(static) num_threads(threads)
-    for (int64_t ni = 0; ni < n; ni++) {
-        for (int64_t kg = 0; kg < k_groups; kg++) {
-            const float scale = scales[ni * k_groups + kg];
-            const float bias = biases[ni * k_groups + kg];
-            for (int64_t kp = 0; kp < gs / 8; kp++) {
-                const uint32_t pkg = qweight[ni * k_packed + kg * (gs / 8) + kp];
-                for (int b = 0; b < 8; b++) {
-                    const float q = (float)((pkg >> (b * 4)) & 0xFu);
-                    const float w = q * scale + bias;
-                    const int64_t k_abs = kg * gs + kp * 8 + b;
-                    for (int64_t mi = 0; mi < m; mi++) out[mi * n + ni] += x[mi * k + k_abs] * w;
+    /* Each output keeps the reference's accumulation: zero, then x*w over k
+     * in (group, word, nibble) order, then the bias.  The rows of one output
+     * column are independent sums, so they run side by side over a
+     * transposed X (xT[k][m]), which vectorises across rows without
+     * reassociating any sum. */
+    float *xT = (float *)malloc(sizeof(float) * (size_t)(m * k));
+    if (!xT) return set_err("qmm_4bit: oom");
+    for (int64_t mi = 0; mi < m; mi++)
+        for (int64_t kk = 0; kk < k; kk++) xT[kk * m + mi] = x[mi * k + kk];
+    int oom = 0;
+#pragma omp parallel num_threads(threads)
+    {
+        float *acc = (float *)malloc(sizeof(float) * (size_t)m);
+        if (!acc) {
+#pragma omp atomic write
+            oom = 1;
+        }
+#pragma omp for schedule(static)
+        for (int64_t ni = 0; ni < n; ni++) {
+            if (!acc) continue;
+            for (int64_t mi = 0; mi < m; mi++) acc[mi] = 0.0f;
+            for (int64_t kg = 0; kg < k_groups; kg++) {
+                const float scale = scales[ni * k_groups + kg];
+                const float bias = biases[ni * k_groups + kg];
+                for (int64_t kp = 0; kp < gs / 8; kp++) {
+                    const uint32_t pkg = qweight[ni * k_packed + kg * (gs / 8) + kp];
+                    for (int b = 0; b < 8; b++) {
+                        const float q = (float)((pkg >> (b * 4)) & 0xFu);
+                        const float w = q * scale + bias;
+                        const float *xc = xT + (kg * gs + kp * 8 + b) * m;
+                        for (int64_t mi = 0; mi < m; mi++) acc[mi] += xc[mi] * w;
+                    }
                 }
             }
+            if (bias_vec)
+                for (int64_t mi = 0; mi < m; mi++) acc[mi] += bias_vec[ni];
+            for (int64_t mi = 0; mi < m; mi++) out[mi * n + ni] = acc[mi];
         }
-        if (bias_vec)
-            for (int64_t mi = 0; mi < m; mi++) out[mi * n + ni] += bias_vec[ni];
+        free(acc);
     }
+    free(xT);
+    if (oom) return set_err("qmm_4bit: oom");
     return 0;
 }
 

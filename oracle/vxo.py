@@ -66,6 +66,7 @@ def _load() -> C.CDLL:
         "vxo_pages_alloc": (C.c_int, [vp, _i64, _u32p]),
         "vxo_pages_free": (None, [vp, _u32p, _i64]),
         "vxo_pages_num_free": (_i64, [vp]),
+        "vxo_pages_pool": (vp, [vp, _i64, C.c_int]),
         "vxo_forward": (C.c_int, [vp, vp, _u32p, vp, _i64, C.c_int, vp, _f32p]),
         "vxo_spec_prefill": (C.c_int, [vp, vp, vp, _i64, vp]),
         "vxo_spec_step": (C.c_int, [vp, vp, _i64, _i64, _i64, _i32p, _u32p, _i32p, vp, vp]),
@@ -354,6 +355,7 @@ class Model:
 class Pages:
     def __init__(self, layers, kv_heads, head_dim, page_size, num_pages):
         self.page_size = page_size
+        self.layers, self.kv_heads, self.head_dim, self.num_pages = layers, kv_heads, head_dim, num_pages
         self.h = lib.vxo_pages_create(layers, kv_heads, head_dim, page_size, num_pages)
         if not self.h:
             raise RuntimeError(lib.vxo_last_error().decode())
@@ -367,6 +369,13 @@ class Pages:
     def free(self, pages):
         p = np.ascontiguousarray(pages, np.uint32)
         lib.vxo_pages_free(self.h, p, p.size)
+
+    def pool(self, layer, kv):
+        """Writable view of one layer's K (kv=0) or V (kv=1) pool
+        [num_pages, kv_heads, page_size, head_dim]."""
+        ptr = lib.vxo_pages_pool(self.h, layer, kv)
+        shape = (self.num_pages, self.kv_heads, self.page_size, self.head_dim)
+        return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_float)), shape=shape)
 
     def num_free(self):
         return lib.vxo_pages_num_free(self.h)

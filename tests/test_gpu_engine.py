@@ -1,13 +1,15 @@
 """GPU engine parity: PagedQwen3 forward / forward_all and SpecEngine rounds
 against the CPU oracle (the reference's spec.rs / qwen3.rs restated).
 
-Token streams are compared round by round.  Like the reference's own spec test
+Spec rounds are checked round by round by an oracle mirror that replays each
+GPU round on the GPU's own tokens (tests/lockstep.py), so every round is
+compared: (a) accept/reject decisions, draft draws and committed tokens are
+bit-exact given the GPU's own logits and uniforms, (b) draft and verify
+logits are within 1e-2 + 1e-2|ref| of the oracle, and (c) wherever the
+oracle's own logits would pick another greedy token, the two sit on a
+near-tie within that tolerance.  Like the reference's own spec test
 (tests/spec_decode.rs:137-148), two implementations with different reduction
-orders can flip an argmax where two bf16 logits tie or nearly tie; the tests
-therefore require (a) bit-exact accept/reject decisions and committed tokens
-given the GPU's own logits, (b) logits within 1e-2 + 1e-2|ref| of the oracle,
-and (c) identical streams up to the first round whose oracle logits hold a
-near-tie at the argmax (anything else fails).
+orders may flip an argmax only at such a tie.
 """
 import numpy as np
 import pytest
@@ -35,14 +37,6 @@ def make_pair(cfg, seed, draft_layers, pages=64, ps=16):
         o_tp=vxo.Pages(L, HK, D, ps, pages), o_dp=vxo.Pages(draft_layers, HK, D, ps, pages),
         g_tp=engine.PagedKvCache(L, HK, D, ps, pages), g_dp=engine.PagedKvCache(draft_layers, HK, D, ps, pages),
     )
-
-
-def near_tie(row: np.ndarray, tol_ulps: float = 1.0) -> bool:
-    """True when the top two values of a bf16 logit row are within `tol_ulps`
-    bf16 ulps of each other (or tie exactly)."""
-    top = np.sort(row)[-2:]
-    ulp = 2.0 ** (np.floor(np.log2(abs(top[1]) + 1e-30)) - 7)
-    return (top[1] - top[0]) <= tol_ulps * ulp
 
 
 def test_forward_matches_oracle(cuda):
@@ -112,51 +106,174 @@ def test_forward_tree_matches_oracle(cuda):
     assert_allclose_elementwise("tree verify logits", got, ref, 1e-2, 1e-2)
 
 
-def run_greedy_pair(cfg, seed, draft_layers, prompts, k, rounds, fix_hole=False):
+def run_lockstep(cfg, w, draft_layers, prompts, k, rounds, temperature=0.0, seed=0, ps=16):
+    """GPU engine rounds, each replayed and checked by the oracle mirror
+    (tests/lockstep.py); returns the accepted counts of every round."""
     from velox_amd import engine
 
-    P = make_pair(cfg, seed, draft_layers, pages=128)
-    oe = vxo.SpecEngine(P["o_t"], P["o_tp"], P["o_d"], P["o_dp"], fix_draft_hole=fix_hole)
-    ge = engine.SpecEngine(P["g_t"], P["g_tp"], P["g_d"], P["g_dp"], fix_draft_hole=fix_hole)
-    os_ = oe.prefill(prompts)
+    from lockstep import Lockstep
+
+    L, HK, D = cfg["layers"], cfg["n_kv_heads"], cfg["head_dim"]
+    max_tokens = max(len(p) for p in prompts) + rounds * (k + 1) + k + 2
+    pages = ((max_tokens + ps - 1) // ps) * len(prompts) + 2
+    g_t = engine.PagedQwen3(cfg, w)
+    g_d = engine.PagedQwen3(cfg, w, n_layers=draft_layers)
+    ge = engine.SpecEngine(g_t, engine.PagedKvCache(L, HK, D, ps, pages), g_d,
+                           engine.PagedKvCache(draft_layers, HK, D, ps, pages), temperature=temperature,
+                           sample_seed=seed)
+    ge.set_tracing(True)
     gs = ge.prefill_batch(prompts)
-    n = len(prompts)
+    ls = Lockstep(cfg, w, draft_layers, max_tokens, len(prompts), ps=ps, temperature=temperature, seed=seed)
+    ls.prefill(prompts)
+    accepted = []
     for r in range(rounds):
-        ro = oe.step(os_, k, trace=True)
-        rg = ge.step_batch(gs, k)
-        cand_g, logits_g = ge.last_trace(n, k)
-        # (a) decisions on the GPU's own logits are bit-exact
-        acc_ref, tok_ref = vxo.accept_greedy(logits_g, cand_g)
-        for b in range(n):
-            assert rg[b].accepted == acc_ref[b], f"round {r} seq {b}: accept decision differs"
-            assert rg[b].committed_tokens == list(tok_ref[b, : acc_ref[b] + 1])
-        # (b) logits agree within tolerance where the inputs agree
-        same_inputs = np.array_equal(cand_g, ro["candidates"])
-        if same_inputs:
-            assert_allclose_elementwise(f"round {r} verify logits", logits_g, ro["logits"], 1e-2, 1e-2)
-        # (c) identical streams unless the oracle had a near-tie
-        for b in range(n):
-            if rg[b].committed_tokens != list(ro["committed"][b]) or not same_inputs:
-                rows = ro["logits"][b]
-                assert any(near_tie(rows[i]) for i in range(k + 1)) or not same_inputs, \
-                    f"round {r} seq {b}: streams diverged without a near-tie"
-                return r, oe, ge, os_, gs
-    return rounds, oe, ge, os_, gs
+        outs = ge.step_batch(gs, k)
+        tr = ge.last_round()
+        assert tr["serial"] == r + 1 and tr["n"] == len(prompts) and tr["k"] == k
+        if temperature > 0:
+            assert np.array_equal(tr["streams"], [s.id for s in gs]) and (tr["rounds"] == r).all()
+        ls.check_round(tr, outs)
+        accepted += [o.accepted for o in outs]
+    assert ls.rounds_checked == rounds
+    for b in range(len(prompts)):
+        assert gs[b].tokens == ls.seqs[b]["tokens"], f"seq {b}: token streams differ"
+        assert gs[b].kv_len == ls.seqs[b]["kv_len"]
+    return accepted
 
 
-def test_spec_greedy_matches_oracle(cuda):
+def zero_mean(w):
+    from test_oracle_model import zero_mean as zm
+
+    return zm(w)
+
+
+@pytest.mark.parametrize("weights", ["config", "zero_mean"])
+def test_spec_greedy_lockstep(cuda, weights):
+    """Six greedy rounds of three sequences (k = 4, 2-layer draft of a
+    4-layer target), every round checked by the oracle.  'config' uses the
+    benchmark's weight distribution (positive mean, degenerate streams);
+    'zero_mean' centres the int4 biases so the draft disagrees and rejections
+    happen."""
     from velox_amd import synth
 
     cfg = synth.tiny_config(layers=4)
+    w = synth.host_weights(cfg, 3)
+    if weights == "zero_mean":
+        w = zero_mean(w)
     rng = np.random.default_rng(7)
     prompts = [rng.integers(0, cfg["vocab"], size=L).astype(np.uint32) for L in (5, 9, 17)]
-    r, oe, ge, os_, gs = run_greedy_pair(cfg, 3, 2, prompts, k=4, rounds=6)
-    assert r >= 1
-    if r == 6:  # no divergence: full streams and KV lengths identical
-        for b in range(3):
-            assert ge.step_batch  # engine alive
-            assert gs[b].tokens == list(vxo.SpecEngine.tokens(os_[b]))
-            assert gs[b].kv_len == os_[b].kv_len
+    acc = run_lockstep(cfg, w, 2, prompts, k=4, rounds=6)
+    if weights == "zero_mean":
+        assert min(acc) < 4, "no round rejected a candidate"
+
+
+@pytest.mark.parametrize("temperature,k", [(0.8, 4), (0.7, 6)])
+def test_spec_stochastic_lockstep(cuda, temperature, k):
+    """Stochastic rounds (Leviathan et al. acceptance) of three sequences:
+    the device Philox uniforms, the draft draws on the GPU's draft logits and
+    every accept / residual decision match the oracle bit for bit, and the
+    logits match within tolerance, every round."""
+    from velox_amd import synth
+
+    cfg = synth.tiny_config(layers=4)
+    w = zero_mean(synth.host_weights(cfg, 6))
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(0, cfg["vocab"], size=L).astype(np.uint32) for L in (6, 11, 4)]
+    acc = run_lockstep(cfg, w, 2, prompts, k=k, rounds=5, temperature=temperature, seed=1234)
+    assert min(acc) < k, "every candidate accepted: the residual draw never ran"
+
+
+def test_spec_stochastic_lockstep_qwen3_0_6b(cuda):
+    """Config 4's sampling path (T = 0.7, k = 6 from a 2-layer draft) at the
+    Qwen3-0.6B shape and the full 151936-token vocabulary: 19 softmax chunks
+    per row in the device statistics and draws."""
+    from velox_amd import synth
+
+    cfg = synth.qwen3_config("qwen3-0.6b", max_pos=512)
+    w = synth.host_weights(cfg, 4)
+    prompts = [synth.prompt(4, n, cfg["vocab"], stream=i) for i, n in enumerate((9, 14, 6))]
+    run_lockstep(cfg, w, 2, prompts, k=6, rounds=2, temperature=0.7, seed=4)
+
+
+def test_spec_metric_shape_lockstep(cuda):
+    """The metric's model: Qwen3-4B shape, int4 g64, k = 4, draft = first 4
+    layers, three sequences, two greedy rounds checked by the oracle."""
+    from velox_amd import synth
+
+    cfg = synth.qwen3_config("qwen3-4b", max_pos=512)
+    w = synth.host_weights(cfg, 1)
+    prompts = [synth.prompt(1, n, cfg["vocab"], stream=i) for i, n in enumerate((8, 12, 5))]
+    run_lockstep(cfg, w, 4, prompts, k=4, rounds=2)
+
+
+def test_tree_verify_step_qwen3_4b(cuda):
+    """One config-3 tree-verify step at the Qwen3-4B shape against the oracle:
+    the 4-2-2 tree under each sequence's last token (vx_forward with tree
+    parents: ancestor masks, depth-based RoPE), greedy longest-path accept on
+    the GPU's logits (bit-exact), the accepted path's K/V moved to consecutive
+    slots (vx_kv_compact_path, mirrored on the oracle's pools), then a chain
+    verify of 5 rows that reads the compacted KV (logits within tolerance)."""
+    import torch
+
+    from velox_amd import engine, ops, synth
+
+    from test_gpu_kernels import tree_4_2_2, u32
+
+    cfg = synth.qwen3_config("qwen3-4b", max_pos=512)
+    w = synth.host_weights(cfg, 3)
+    par = tree_4_2_2()
+    R, B, ps = len(par), 2, 16
+    L, HK, D, V = cfg["layers"], cfg["n_kv_heads"], cfg["head_dim"], cfg["vocab"]
+    g = engine.PagedQwen3(cfg, w)
+    gp = engine.PagedKvCache(L, HK, D, ps, 16)
+    from lockstep import oracle_threads
+
+    o = vxo.Model(dict(cfg, dtype=vxo.BF16), synth.as_model_dtype(w, "bf16"), threads=oracle_threads())
+    op = vxo.Pages(L, HK, D, ps, 16)
+    prompts = [synth.prompt(3, n, V, stream=i) for i, n in enumerate((21, 13))]
+    nb = 4
+    gbt = [gp.alloc(nb) for _ in range(B)]
+    obt = [op.alloc(nb) for _ in range(B)]
+    # prefill prompt[..len-1] on both
+    ids = np.concatenate([p[:-1] for p in prompts])
+    g.forward(gp, ids, [(len(p) - 1, 0, bt) for p, bt in zip(prompts, gbt)])
+    vxo.forward(o, op, ids, [(len(p) - 1, 0, bt) for p, bt in zip(prompts, obt)], all_rows=False)
+    kvo = [len(p) - 1 for p in prompts]
+    rng = np.random.default_rng(5)
+    nodes = np.concatenate([np.concatenate([[p[-1]], rng.integers(0, V, size=R - 1)]) for p in prompts])
+    nodes = nodes.astype(np.uint32)
+    print("[tree-4b] prefill done", flush=True)
+    got = g.forward_all(gp, nodes, [(R, kvo[b], gbt[b]) for b in range(B)], tree_parents=par)
+    ref = vxo.forward(o, op, nodes, [(R, kvo[b], obt[b]) for b in range(B)], all_rows=True, tree_parents=par)
+    print("[tree-4b] tree forward done", flush=True)
+    lg = got.float().cpu().numpy()
+    assert_allclose_elementwise("4B tree verify logits", lg, ref, 1e-2, 1e-2)
+    acc, path, tok = ops.accept_tree(got.view(B, R, V), par, u32(nodes.reshape(B, R)))
+    torch.cuda.synchronize()
+    acc_h, path_h, tok_h = acc.cpu().numpy(), path.cpu().numpy(), tok.cpu().numpy()
+    ra, rp, rt = vxo.accept_tree(lg.reshape(B, R, V), np.asarray(par, np.int32), nodes.reshape(B, R))
+    assert np.array_equal(acc_h, ra)
+    for b in range(B):
+        assert np.array_equal(path_h[b, : ra[b] + 1], rp[b, : ra[b] + 1])
+        assert np.array_equal(tok_h[b, : ra[b] + 1].astype(np.uint32), rt[b, : ra[b] + 1])
+    # move the accepted paths to consecutive slots on both sides
+    ops.kv_compact_path(gp, u32(np.stack(gbt)), u32(np.array(kvo)), acc, path)
+    for layer in range(L):
+        for kv in (0, 1):
+            pool = op.pool(layer, kv)
+            for b in range(B):
+                src = [int(kvo[b]) + int(rp[b, d]) for d in range(1, ra[b] + 1)]
+                rows = [pool[obt[b][x // ps], :, x % ps].copy() for x in src]
+                for d, row in enumerate(rows, start=1):
+                    x = int(kvo[b]) + d
+                    pool[obt[b][x // ps], :, x % ps] = row
+    # a chain verify over [bonus, 4 more tokens] after the compacted path
+    nxt = [kvo[b] + int(ra[b]) + 1 for b in range(B)]
+    chain = np.concatenate([np.concatenate([[rt[b, ra[b]]], rng.integers(0, V, size=4)]) for b in range(B)])
+    chain = chain.astype(np.uint32)
+    got = g.forward_all(gp, chain, [(5, nxt[b], gbt[b]) for b in range(B)]).float().cpu().numpy()
+    ref = vxo.forward(o, op, chain, [(5, nxt[b], obt[b]) for b in range(B)], all_rows=True)
+    assert_allclose_elementwise("4B chain verify after compaction", got, ref, 1e-2, 1e-2)
 
 
 def test_spec_draft_equals_target_accepts_all(cuda):
@@ -199,36 +316,33 @@ def test_spec_errors_and_capacity(cuda):
         engine.SpecEngine(t, tp, t, dp16).prefill(np.arange(2, 5, dtype=np.uint32))
 
 
-def test_spec_stochastic_deterministic(cuda):
-    from velox_amd import engine, synth
-
-    cfg = synth.tiny_config(layers=2)
-    w = synth.host_weights(cfg, 6)
-    streams = []
-    for _ in range(2):
-        t = engine.PagedQwen3(cfg, w)
-        d = engine.PagedQwen3(cfg, w, n_layers=1)
-        tp = engine.PagedKvCache(2, cfg["n_kv_heads"], cfg["head_dim"], 16, 64)
-        dp = engine.PagedKvCache(1, cfg["n_kv_heads"], cfg["head_dim"], 16, 64)
-        e = engine.SpecEngine(t, tp, d, dp, temperature=0.8, sample_seed=11)
-        ss = e.prefill_batch([np.arange(1, 9, dtype=np.uint32), np.arange(40, 45, dtype=np.uint32)])
-        for _ in range(5):
-            e.step_batch(ss, 4)
-        streams.append([s.tokens for s in ss])
-    assert streams[0] == streams[1]
-    for toks in streams[0]:
-        assert all(0 <= t < cfg["vocab"] for t in toks)
-
-
-def test_config0_qwen3_0_6b_shape(cuda):
-    """Config 0 at a CPU-checkable length: Qwen3-0.6B shape, draft = first 4
-    layers, k = 4, batch 1, seed 0 (8-token prompt, 3 rounds)."""
+def test_config0_full_workload(cuda):
+    """Config 0 end to end: Qwen3-0.6B shape, draft = first 4 layers, k = 4,
+    batch 1, a 128-token prompt and 64 generated tokens (seed 0), every round
+    checked by the oracle."""
     from velox_amd import synth
 
     cfg = synth.qwen3_config("qwen3-0.6b", max_pos=512)
-    prompt = synth.prompt(0, 8, cfg["vocab"])
-    r, *_ = run_greedy_pair(cfg, 0, 4, [prompt], k=4, rounds=3)
-    assert r >= 1
+    w = synth.host_weights(cfg, 0)
+    prompt = synth.prompt(0, 128, cfg["vocab"])
+    rounds = 64  # an upper bound: at least one token per round
+    from velox_amd import engine
+
+    from lockstep import Lockstep
+
+    L, HK, D = cfg["layers"], cfg["n_kv_heads"], cfg["head_dim"]
+    g_t, g_d = engine.PagedQwen3(cfg, w), engine.PagedQwen3(cfg, w, n_layers=4)
+    ge = engine.SpecEngine(g_t, engine.PagedKvCache(L, HK, D, 16, 16), g_d, engine.PagedKvCache(4, HK, D, 16, 16))
+    ge.set_tracing(True)
+    gs = ge.prefill(prompt)
+    ls = Lockstep(cfg, w, 4, 128 + 64 + 8, 1)
+    ls.prefill([prompt])
+    while len(gs.tokens) < 128 + 64 and rounds:
+        outs = ge.step_batch([gs], 4)
+        ls.check_round(ge.last_round(), outs)
+        rounds -= 1
+    assert len(gs.tokens) >= 128 + 64
+    assert gs.tokens == ls.seqs[0]["tokens"]
 
 
 def test_mlx_checkpoint_loads_and_runs(cuda, tmp_path):

@@ -271,6 +271,49 @@ def test_qmm_pack_layout_round_trip(cuda, shape):
     assert np.array_equal(bi, lin["biases"].view(np.uint16))
 
 
+def test_qmm_bias_rounds_once(cuda):
+    """qmm_4bit with a bias rounds once (metal_kernels.rs:473-474:
+    acc += bias; Y = (T)acc): the f16 result equals round_f16(acc + bias)
+    bit for bit, where acc is the same GEMM's f32 accumulator (read through
+    the extended entry point with f32 rounding and output)."""
+    from velox_amd import _lib, ops
+
+    m, n, k = 3, 256, 512
+    rng = np.random.default_rng(12)
+    x = torch.from_numpy(rng.normal(0, 1, size=(m, k)).astype(np.float16)).cuda()
+    lin = synth_linear(n, k, 13)
+    qw = torch.from_numpy(lin["qweight"].view(np.int32)).cuda()
+    sc = torch.from_numpy(lin["scales"]).cuda()
+    bs = torch.from_numpy(lin["biases"]).cuda()
+    bias = torch.from_numpy(rng.normal(0, 1, size=n).astype(np.float16)).cuda()
+    y = ops.qmm_4bit(x, qw, sc, bs, bias=bias)
+    acc = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.qmm_4bit_ex(x, qw, sc, bs, acc, round_dtype=_lib.F32)
+    torch.cuda.synchronize()
+    want = (acc.cpu().numpy() + bias.float().cpu().numpy()).astype(np.float16)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+def test_prefill_rejects_inconsistent_seq_ids(cuda):
+    """seq_id_per_q must name, for every row, the sequence whose cu_seqlens
+    range holds it (the reference kernel reads it, MSL :307-395)."""
+    from velox_amd import ops
+    from velox_amd._lib import VeloxError
+
+    q = torch.zeros(6, 4, 64, dtype=torch.float16, device="cuda")
+    pool = torch.zeros(4, 2, 16, 64, dtype=torch.float16, device="cuda")
+    bt = u32(np.array([[0, 1], [2, 3]]))
+    cu = u32(np.array([0, 4, 6]))
+    kvo = u32(np.array([0, 3]))
+    ops.paged_prefill_attention(q, pool, pool, bt, cu, u32(np.array([0, 0, 0, 0, 1, 1])), kvo, 0.125)
+    with pytest.raises(VeloxError, match="disagrees with cu_seqlens"):
+        ops.paged_prefill_attention(q, pool, pool, bt, cu, u32(np.array([0, 0, 0, 1, 1, 1])), kvo, 0.125)
+    with pytest.raises(VeloxError, match="disagrees with cu_seqlens"):
+        ops.paged_prefill_attention(q, pool, pool, bt, cu, u32(np.array([0, 0, 0, 0, 1, 2])), kvo, 0.125)
+    with pytest.raises(VeloxError, match="run from 0 to total_q"):
+        ops.paged_prefill_attention(q, pool, pool, bt, u32(np.array([0, 4, 5])), u32(np.zeros(6)), kvo, 0.125)
+
+
 def test_qmm_validation_errors(cuda):
     from velox_amd import ops
     from velox_amd._lib import VeloxError
@@ -439,6 +482,49 @@ def test_verify_attention_tree(cuda):
     perm = rng.permutation(B * nb).reshape(B, nb)
     got, ref = _prefill_case([R] * B, [ctx] * B, perm, B * nb, 9, dt="f16", hq=32, hk=8, tree=par)
     assert_allclose_elementwise("tree attention", got, ref, 1e-2, 1e-2)
+
+
+def test_tree_attention_config3_geometry(cuda):
+    """Config 3 at its own geometry: 16 sequences at context 2048, each
+    verifying the 4-2-2 tree plus its root (17 rows, 68 query vectors per KV
+    head: the 32-vector query tiles and the KV-split merge both run), GQA
+    32/8, head_dim 128, f16 KV on a shuffled block table."""
+    par = tree_4_2_2()
+    R, B, ps, ctx = len(par), 16, 16, 2048
+    nb = (ctx + R + ps - 1) // ps
+    rng = np.random.default_rng(33)
+    P = B * nb + 5
+    perm = rng.permutation(P)[: B * nb].reshape(B, nb)
+    got, ref = _prefill_case([R] * B, [ctx] * B, perm, P, 303, dt="f16", hq=32, hk=8, tree=par)
+    assert_allclose_elementwise("config-3 tree attention", got, ref, 1e-2, 1e-2)
+
+
+def test_chain_attention_config4_geometry(cuda):
+    """Config 4's verify attention: 32 sequences, k = 6 (7 rows each),
+    contexts up to 4096 tokens, and the first 512 tokens (32 pages) shared by
+    every group of 8 sequences through their block tables, the rest of each
+    table on shuffled private pages."""
+    B, R, ps, k_shared = 32, 7, 16, 32
+    rng = np.random.default_rng(44)
+    ctx = rng.integers(600, 4096 - R, size=B)
+    ctx[0] = 4096 - R
+    nb = (ctx + R + ps - 1) // ps
+    groups = B // 8
+    private = int((nb - k_shared).sum())
+    P = groups * k_shared + private + 3
+    perm = rng.permutation(P)
+    shared = perm[: groups * k_shared].reshape(groups, k_shared)
+    own = perm[groups * k_shared:]
+    mb = int(nb.max())
+    bt = np.zeros((B, mb), np.uint32)
+    o = 0
+    for b in range(B):
+        bt[b, :k_shared] = shared[b // 8]
+        n_own = int(nb[b]) - k_shared
+        bt[b, k_shared: k_shared + n_own] = own[o: o + n_own]
+        o += n_own
+    got, ref = _prefill_case([R] * B, ctx, bt, P, 404, dt="f16", hq=32, hk=8)
+    assert_allclose_elementwise("config-4 chain attention", got, ref, 1e-2, 1e-2)
 
 
 def test_chain_tree_equals_causal(cuda):

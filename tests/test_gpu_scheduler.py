@@ -84,6 +84,56 @@ def test_scheduler_greedy_prefix_sharing_and_chunks(cuda):
     assert tp.num_free_pages() == 256 and dp.num_free_pages() == 256
 
 
+def test_scheduler_stochastic_lockstep(cuda):
+    """Config 4's sampling path through the scheduler: T = 0.7, per-request
+    Philox streams (the request id), k = 4, chunked prefill and prefix-shared
+    pages.  Every speculative round the scheduler runs is replayed by the
+    oracle mirror (tests/lockstep.py) on the GPU's own logits: uniforms,
+    draft draws and accept / residual decisions bit-exact, logits within
+    tolerance; each request's tokens equal the mirror's committed stream."""
+    from velox_amd import engine, synth
+    from velox_amd.scheduler import BatchScheduler, RequestStatus, SchedulerConfig
+
+    from lockstep import Lockstep
+    from test_oracle_model import zero_mean
+
+    cfg = synth.tiny_config(layers=4)
+    w = zero_mean(synth.host_weights(cfg, 23))
+    t, d = engine.PagedQwen3(cfg, w), engine.PagedQwen3(cfg, w, n_layers=2)
+    HK, D = cfg["n_kv_heads"], cfg["head_dim"]
+    e = engine.SpecEngine(t, engine.PagedKvCache(4, HK, D, PS, 192), d, engine.PagedKvCache(2, HK, D, PS, 192),
+                          temperature=0.7, sample_seed=5, fix_draft_hole=True)
+    e.set_tracing(True)
+    rng = np.random.default_rng(9)
+    shared = rng.integers(0, cfg["vocab"], 32)
+    prompts = [np.concatenate([shared, rng.integers(0, cfg["vocab"], 3 + 5 * i)]) for i in range(3)]
+    prompts += [rng.integers(0, cfg["vocab"], n) for n in (9, 41)]
+    new = 12
+    s = BatchScheduler(e, (), SchedulerConfig(max_batch_tokens=48, prefix_cache_capacity=32, draft_k=4))
+    ids = [s.submit(p, new, temperature=0.7) for p in prompts]
+    ls = Lockstep(cfg, w, 2, max(len(p) for p in prompts) + new + 12, len(prompts), temperature=0.7, seed=5,
+                  fix_hole=True)
+    ls.prefill(prompts, streams=ids)
+    index_of = {rid: i for i, rid in enumerate(ids)}
+    serial, steps = 0, 0
+    while s.num_waiting() + s.num_running() > 0 and steps < 300:
+        s.step()
+        steps += 1
+        tr = e.last_round()
+        if tr is not None and tr["serial"] != serial:
+            assert tr["serial"] == serial + 1, "more than one round per scheduler step"
+            serial = tr["serial"]
+            ls.check_round(tr, None, seq_index=[index_of[int(x)] for x in tr["streams"]])
+    st = s.stats()
+    assert st["requests_completed"] == len(prompts) and st["prefix_cache_hits"] >= 2
+    assert ls.rounds_checked == serial > 0
+    for rid, p in zip(ids, prompts):
+        r = s.poll(rid)
+        assert r.status == RequestStatus.FINISHED and len(r.tokens) == new
+        assert r.tokens == ls.seqs[index_of[rid]]["tokens"][len(p): len(p) + new], f"request {rid}: tokens differ"
+    s.close()
+
+
 def test_scheduler_stochastic_is_deterministic(cuda):
     """Temperature 0.7 with per-request Philox streams: the same submissions
     give the same tokens on a fresh engine."""

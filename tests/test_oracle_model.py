@@ -182,3 +182,39 @@ def test_spec_errors_and_capacity(tiny):
     e2 = vxo.SpecEngine(t, vxo.Pages(L, HK, D, 16, 2), t, vxo.Pages(L, HK, D, 8, 2))
     with pytest.raises(RuntimeError, match="page_size"):
         e2.prefill([np.arange(2, 5, dtype=np.uint32)])
+
+
+def test_lockstep_mirror_replays_the_oracle_engine(tiny, monkeypatch):
+    """The round-by-round mirror the GPU engine tests use (tests/lockstep.py)
+    restates the spec loop's KV bookkeeping (draft fed [last, c0..c_{D-2}] at
+    kv_len + i, the draft-KV hole, verify at kv_len, commit A + 1): replayed
+    on the oracle engine's own rounds it reproduces their verify logits bit for
+    bit and the same token streams."""
+    import lockstep
+
+    monkeypatch.setattr(lockstep, "ATOL", 0.0)
+    monkeypatch.setattr(lockstep, "RTOL", 0.0)
+    cfg, w = tiny
+    wb = synth.as_model_dtype(w, "bf16")
+    c = dict(cfg, dtype=vxo.BF16)
+    t, d = vxo.Model(c, wb), vxo.Model(c, wb, n_layers=1)
+    L, HK, D = cfg["layers"], cfg["n_kv_heads"], cfg["head_dim"]
+    prompts = [np.array([5, 77, 301, 12, 9], np.uint32), np.array([8, 1, 400, 22, 13, 100, 7, 250, 3], np.uint32)]
+    e = vxo.SpecEngine(t, vxo.Pages(L, HK, D, 16, 16), d, vxo.Pages(1, HK, D, 16, 16))
+    st = e.prefill(prompts)
+    ls = lockstep.Lockstep(cfg, w, 1, max_tokens=96, n_seqs=2, threads=1)
+    ls.prefill(prompts)
+
+    class Out:
+        def __init__(self, a, toks):
+            self.accepted, self.committed_tokens = int(a), list(map(int, toks))
+
+    accepted = []
+    for _ in range(6):
+        ro = e.step(st, 4, trace=True)
+        tr = {"n": 2, "k": 4, "temperature": 0.0, "candidates": ro["candidates"], "verify_logits": ro["logits"]}
+        ls.check_round(tr, [Out(ro["accepted"][b], ro["committed"][b]) for b in range(2)])
+        accepted += list(ro["accepted"])
+    for b in range(2):
+        assert ls.seqs[b]["tokens"] == vxo.SpecEngine.tokens(st[b]).tolist()
+    assert min(accepted) < 4 and max(accepted) >= 1, accepted  # rejections and accepted candidates

@@ -84,6 +84,11 @@ class StepProfile(C.Structure):
                 ("draft_kernel_bytes", C.c_double * 3), ("draft_kernel_launches", C.c_int64 * 3)]
 
 
+class RoundTrace(C.Structure):
+    _fields_ = [("n", i64), ("draft_k", i64), ("vocab", i64), ("temperature", f32), ("has_draft_logits", C.c_int32),
+                ("serial", C.c_uint64)]
+
+
 class SchedConfig(C.Structure):
     _fields_ = [("max_running_requests", i64), ("max_batch_tokens", i64), ("prefix_cache_capacity", i64),
                 ("draft_k", i64)]
@@ -153,6 +158,9 @@ _SIGS = {
     "vx_spec_state_num_tokens": (i64, [vp, i64]),
     "vx_spec_state_tokens": (i32, [vp, i64, u32p, i64]),
     "vx_spec_last_trace": (i32, [vp, u32p, C.POINTER(f32)]),
+    "vx_spec_set_tracing": (i32, [vp, i32]),
+    "vx_spec_last_trace_info": (i32, [vp, C.POINTER(RoundTrace), C.POINTER(i64), u32p, u32p]),
+    "vx_spec_last_trace_draft": (i32, [vp, C.POINTER(f32), C.POINTER(f32)]),
     "vx_spec_free": (None, [vp, i64]),
     "vx_spec_set_profiling": (i32, [vp, i32]),
     "vx_spec_last_profile": (i32, [vp, C.POINTER(StepProfile)]),

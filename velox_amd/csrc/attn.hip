@@ -21,6 +21,9 @@
 // f32 tensors use a plain per-(row, head) kernel with the reference's loop.
 #include <hip/hip_runtime.h>
 
+#include <string>
+#include <vector>
+
 #include <algorithm>
 #include <cstdlib>
 
@@ -791,7 +794,26 @@ extern "C" int vx_paged_attention(const void *q, const void *k_pool, const void 
     VX_REQUIRE(q && k_pool && v_pool && block_table && cu_seqlens && kv_offsets && out,
                "paged_attention: null tensor");
     VX_REQUIRE(max_blocks > 0 && num_pages > 0 && page_size > 0, "paged_attention: empty pool");
-    (void)seq_id_per_q;  // rows are located through cu_seqlens
+    VX_REQUIRE(seq_id_per_q, "paged_attention: null tensor");
+    // The reference's kernel finds a row's sequence through seq_id_per_q and
+    // its position through cu_seqlens (MSL :307-395); this kernel walks the
+    // cu_seqlens ranges, so the two must describe the same rows.  They are
+    // checked on the host (one small copy and a stream synchronisation).
+    {
+        hipStream_t st = (hipStream_t)stream;
+        std::vector<uint32_t> cu((size_t)n_seqs + 1), sid((size_t)total_q);
+        VX_HIP(hipMemcpyAsync(cu.data(), cu_seqlens, cu.size() * 4, hipMemcpyDeviceToHost, st));
+        VX_HIP(hipMemcpyAsync(sid.data(), seq_id_per_q, sid.size() * 4, hipMemcpyDeviceToHost, st));
+        VX_HIP(hipStreamSynchronize(st));
+        VX_REQUIRE(cu[0] == 0 && (int64_t)cu[n_seqs] == total_q, "paged_attention: cu_seqlens must run from 0 to total_q");
+        for (int64_t s = 0; s < n_seqs; s++)
+            VX_REQUIRE(cu[s] <= cu[s + 1], "paged_attention: cu_seqlens must be non-decreasing");
+        for (int64_t row = 0; row < total_q; row++) {
+            const uint32_t sq = sid[row];
+            VX_REQUIRE(sq < (uint64_t)n_seqs && cu[sq] <= (uint64_t)row && (uint64_t)row < cu[sq + 1],
+                       "paged_attention: seq_id_per_q[" + std::to_string(row) + "] disagrees with cu_seqlens");
+        }
+    }
     // rows per sequence and KV length are bounded by total_q and the block table
     return paged_attention_launch(q, k_pool, v_pool, block_table, cu_seqlens, kv_offsets, tree_mask,
                                   out, 0, total_q, n_seqs, total_q, max_blocks, num_pages, h_q, h_kv,

@@ -45,6 +45,15 @@ int hip_error(hipError_t e, const char *what) {
     return -2;
 }
 
+int check_tree_parents(const int32_t *parents, int64_t r, const char *who) {
+    const std::string w(who);
+    VX_REQUIRE(r >= 1 && r <= 64, w + ": a tree holds 1..64 nodes");
+    VX_REQUIRE(parents && parents[0] < 0, w + ": node 0 must be the root");
+    for (int64_t j = 1; j < r; j++)
+        VX_REQUIRE(parents[j] >= 0 && parents[j] < j, w + ": parents[j] must precede j");
+    return 0;
+}
+
 int device_cu_count() {
     static std::mutex mu;
     static std::map<int, int> cache;
@@ -59,9 +68,15 @@ int device_cu_count() {
     return cus;
 }
 
+// Library-owned workspace per (device, stream) for the entry points called
+// without one.  It grows geometrically; a superseded buffer is never freed
+// while the library is loaded, because another host thread on the same
+// stream may still be queueing kernels that read it (at most the final size
+// again is held in retired buffers).
 int stream_workspace(hipStream_t s, size_t bytes, void **out) {
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> ws;
+    static std::vector<void *> retired;
     int dev = 0;
     VX_HIP(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(mu);
@@ -72,15 +87,10 @@ int stream_workspace(hipStream_t s, size_t bytes, void **out) {
     }
     size_t sz = std::max(bytes, e.second * 2);
     sz = (sz + 4095) & ~(size_t)4095;
-    if (e.first) {
-        VX_HIP(hipStreamSynchronize(s));
-        VX_HIP(hipFree(e.first));
-        e.first = nullptr;
-        e.second = 0;
-    }
     void *p = nullptr;
     VX_HIP(hipMalloc(&p, sz));
     VX_HIP(hipMemsetAsync(p, 0, sz, s));
+    if (e.first) retired.push_back(e.first);
     e.first = p;
     e.second = sz;
     *out = p;
@@ -886,6 +896,9 @@ int prepare_ws(vx_model *m, const Meta &meta, int all_rows) {
 extern "C" int vx_forward(vx_model *m, vx_pages *pages, const uint32_t *input_ids, const vx_seq_slice *seqs,
                           int64_t n_seqs, int all_rows, const int32_t *tree_parents, void *logits,
                           void *stream) {
+    // the tree is checked before anything reads it (its ancestor walk
+    // assumes parents[j] < j)
+    if (tree_parents && seqs && n_seqs > 0) VX_TRY(check_tree_parents(tree_parents, seqs[0].new_tokens, "forward"));
     VX_REQUIRE(m && pages && input_ids && seqs && logits, "forward: null argument");
     hipStream_t st = (hipStream_t)stream;
     std::vector<SeqDesc> sd(n_seqs);
@@ -942,6 +955,13 @@ struct vx_spec {
     std::vector<uint32_t> last_cand;
     std::vector<float> last_logits;
     int64_t last_n = 0, last_k = 0;
+    // round trace: with tracing on, every draft step keeps its logits
+    bool tracing = false;
+    bool last_kept_draft = false;
+    float last_temp = 0.f;
+    uint64_t serial = 0;
+    std::vector<int64_t> last_ids;
+    std::vector<uint32_t> last_streams, last_rounds;
     Prof prof_draft, prof_verify;
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     bool profiling = false;
@@ -1231,7 +1251,8 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     VX_TRY(e->d_vids.ensure(n * (D + 1) * 4));
     VX_TRY(e->d_tlog.ensure((size_t)n * (D + 1) * V * 2));
     const bool stoch = temp > 0.f;
-    VX_TRY(e->d_dlog.ensure((size_t)n * (stoch ? D : 1) * V * 2));
+    const bool keep_draft = stoch || e->tracing;  // draft logits laid out [D][n][V] (step-major)
+    VX_TRY(e->d_dlog.ensure((size_t)n * (keep_draft ? D : 1) * V * 2));
     VX_TRY(e->d_uni.ensure(n * (D + 1) * 16));
     VX_TRY(e->d_draw.ensure(n * 4));
     const int64_t amax_chunks = vx_cdiv(V, 128);
@@ -1277,7 +1298,7 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     }
     // ---- draft phase: feed [last, c0 .. c_{D-2}] (spec.rs:223-240)
     for (int64_t i = 0; i < D; i++) {
-        void *dl = stoch ? (void *)((uint16_t *)e->d_dlog.p + (size_t)i * n * V) : e->d_dlog.p;
+        void *dl = keep_draft ? (void *)((uint16_t *)e->d_dlog.p + (size_t)i * n * V) : e->d_dlog.p;
         bool fused_amax = false;
         // step i's input: the last tokens, then column i - 1 of cand [n, D]
         const uint32_t *in_ids = i == 0 ? d_last : cand + (i - 1);
@@ -1356,6 +1377,12 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     e->last_n = n;
     e->last_k = D;
     e->last_cand.assign(h_cand, h_cand + n * D);
+    e->last_kept_draft = keep_draft;
+    e->last_temp = temp;
+    e->serial++;
+    e->last_ids.assign(state_ids, state_ids + n);
+    e->last_streams.assign(h_strm, h_strm + n);
+    e->last_rounds.assign(h_rnd, h_rnd + n);
     // ---- commit (spec.rs:294-309)
     for (int64_t b = 0; b < n; b++) {
         SpecState &s = *S[b];
@@ -1407,6 +1434,50 @@ extern "C" int vx_spec_last_trace(const vx_spec *e, uint32_t *candidates, float 
         std::vector<uint16_t> tmp((size_t)n);
         VX_HIP(hipMemcpy(tmp.data(), e->d_tlog.p, (size_t)n * 2, hipMemcpyDeviceToHost));
         for (int64_t i = 0; i < n; i++) verify_logits[i] = bf2f(tmp[i]);
+    }
+    return 0;
+}
+extern "C" int vx_spec_set_tracing(vx_spec *e, int enable) {
+    VX_REQUIRE(e, "tracing: null engine");
+    e->tracing = enable != 0;
+    return 0;
+}
+extern "C" int vx_spec_last_trace_info(const vx_spec *e, vx_round_trace *info, int64_t *state_ids,
+                                       uint32_t *stream_ids, uint32_t *rounds) {
+    VX_REQUIRE(e && info, "trace: null argument");
+    *info = vx_round_trace{};
+    info->serial = e->serial;
+    if (e->serial == 0) return 0;
+    info->n = e->last_n;
+    info->draft_k = e->last_k;
+    info->vocab = e->target->cfg.vocab;
+    info->temperature = e->last_temp;
+    info->has_draft_logits = e->last_kept_draft ? 1 : 0;
+    if (state_ids) memcpy(state_ids, e->last_ids.data(), e->last_ids.size() * 8);
+    if (stream_ids) memcpy(stream_ids, e->last_streams.data(), e->last_streams.size() * 4);
+    if (rounds) memcpy(rounds, e->last_rounds.data(), e->last_rounds.size() * 4);
+    return 0;
+}
+extern "C" int vx_spec_last_trace_draft(const vx_spec *e, float *draft_logits, float *uniforms) {
+    VX_REQUIRE(e && e->last_n > 0, "trace: no step yet");
+    const int64_t n = e->last_n, D = e->last_k, V = e->target->cfg.vocab;
+    if (draft_logits) {
+        VX_REQUIRE(e->last_kept_draft, "trace: the last greedy round kept no draft logits (enable tracing)");
+        std::vector<uint16_t> tmp((size_t)(D * n * V));
+        VX_HIP(hipMemcpy(tmp.data(), e->d_dlog.p, tmp.size() * 2, hipMemcpyDeviceToHost));
+        // device layout [D][n][V] -> [n][D][V]
+        for (int64_t i = 0; i < D; i++)
+            for (int64_t b = 0; b < n; b++) {
+                const uint16_t *src = tmp.data() + (i * n + b) * V;
+                float *dst = draft_logits + (b * D + i) * V;
+                for (int64_t j = 0; j < V; j++) dst[j] = bf2f(src[j]);
+            }
+    }
+    if (uniforms) {
+        if (e->last_temp > 0.f)
+            VX_HIP(hipMemcpy(uniforms, e->d_uni.p, (size_t)n * (D + 1) * 16, hipMemcpyDeviceToHost));
+        else
+            memset(uniforms, 0, (size_t)n * (D + 1) * 16);
     }
     return 0;
 }

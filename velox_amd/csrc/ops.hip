@@ -1056,10 +1056,7 @@ extern "C" int vx_accept_greedy(const void *logits, const uint32_t *candidates, 
 extern "C" int vx_accept_tree(const void *logits, const int32_t *parents, const uint32_t *node_tokens,
                               int32_t *accepted, int32_t *path, uint32_t *tokens, int64_t batch,
                               int64_t r, int64_t vocab, int logits_dtype, void *stream) {
-    VX_REQUIRE(r >= 1 && r <= 64, "accept_tree: 1..64 nodes");
-    VX_REQUIRE(parents && parents[0] < 0, "accept_tree: node 0 must be the root");
-    for (int64_t j = 1; j < r; j++)
-        VX_REQUIRE(parents[j] >= 0 && parents[j] < j, "accept_tree: parents[j] must precede j");
+    VX_TRY(check_tree_parents(parents, r, "accept_tree"));
     if (batch == 0) return 0;
     return argmax_accept_launch(logits, logits_dtype, batch * r, vocab, 2, (int)r, node_tokens, 0, accepted,
                                 tokens, path, parents, nullptr, nullptr, 0, nullptr, 0, (hipStream_t)stream);

@@ -79,6 +79,9 @@ struct QmmArgs {
     // [row * ceil(N/128) + block]; NaN never wins, ties keep the smaller index
     float *amax_v;
     uint32_t *amax_i;
+    // optional per-column bias [N] in y_dt, added to the f32 accumulator
+    // before its single rounding (STORE, metal_kernels.rs:473-474)
+    const void *bias;
 };
 
 typedef unsigned short ushort8 __attribute__((ext_vector_type(8)));
@@ -182,7 +185,9 @@ __device__ __forceinline__ float load_dt(const void *p, int64_t i, int dt) {
 // Epilogue of one output element (STORE / RESIDUAL).
 __device__ __forceinline__ void epi_elem(const QmmArgs &a, int row, int col, float acc) {
     const int64_t idx = (int64_t)row * a.N + col;
-    float v = round_dt(acc * a.acc_scale, a.round_dt);
+    float v = acc * a.acc_scale;
+    if (a.bias) v += load_dt(a.bias, col, a.y_dt);
+    v = round_dt(v, a.round_dt);
     if (a.epi == VX_EPI_RESIDUAL) v = round_dt(load_dt(a.resid, idx, a.y_dt) + v, a.round_dt);
     store_dt(a.y, idx, v * a.store_scale, a.y_dt);
 }
@@ -1478,12 +1483,6 @@ __global__ void qmm_naive_kernel(const void *x, const uint32_t *qw, const void *
     st_elem<DT>(y, idx, acc);
 }
 
-template <int DT>
-__global__ void add_bias_kernel(void *y, const void *bias, int64_t m, int64_t n) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= m * n) return;
-    st_elem<DT>(y, idx, ld_elem<DT>(y, idx) + ld_elem<DT>(bias, idx % n));
-}
 
 struct Plan {
     bool stream;  // f16 streaming kernel (else the LDS-chunked kernel)
@@ -1758,7 +1757,8 @@ size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi, bool packed
 int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, void *y,
                const void *resid, int64_t M, int64_t N, int64_t K, int x_dt, int x_shift,
                int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
-               hipStream_t st, bool packed = false, float *amax_v = nullptr, uint32_t *amax_i = nullptr) {
+               hipStream_t st, bool packed = false, float *amax_v = nullptr, uint32_t *amax_i = nullptr,
+               const void *bias = nullptr) {
     Plan p = packed ? make_plan_p32(M, N, K, epi) : make_plan(M, N, K, epi, x_dt == VX_F16);
     if (epi == VX_EPI_SWIGLU && (N % 32 != 0 || (!p.p32 && p.NT % 2 != 0)))
         return set_error("qmm swiglu: N must be a multiple of 32 with paired tiles");
@@ -1770,9 +1770,11 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
             return set_error("qmm: workspace too small (see vx_qmm_workspace_size)");
         }
     }
+    if (bias && (packed || epi != VX_EPI_STORE)) return set_error("qmm: a bias goes with the row-major STORE GEMM");
     QmmArgs a{};
     a.amax_v = amax_v;
     a.amax_i = amax_i;
+    a.bias = bias;
     a.x = x;
     a.w = w;
     a.s = (const uint16_t *)s;
@@ -1806,9 +1808,10 @@ int qmm_launch(const void *x, const uint32_t *w, const void *s, const void *b, v
 
 int qmm_fast(const void *x, const uint32_t *w, const void *s, const void *b, void *y,
              const void *resid, int64_t M, int64_t N, int64_t K, int x_dt, int x_shift,
-             int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes, hipStream_t st) {
+             int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes, hipStream_t st,
+             const void *bias = nullptr) {
     return qmm_launch(x, w, s, b, y, resid, M, N, K, x_dt, x_shift, 0, round_dt, y_dt, epi, workspace,
-                      ws_bytes, st);
+                      ws_bytes, st, false, nullptr, nullptr, bias);
 }
 
 size_t qmm_packed_bytes(int64_t n, int64_t k) { return (size_t)(n / 32) * (size_t)(k / 128) * kPackBlock; }
@@ -1909,17 +1912,9 @@ extern "C" int vx_qmm_4bit(const void *x, const uint32_t *qweight, const void *s
     VX_REQUIRE(x && qweight && scales && biases && y, "qmm_4bit: null tensor");
     hipStream_t st = (hipStream_t)stream;
     if (dtype != VX_F32 && fast_ok(dtype, k, group_size, x, qweight, scales, biases) && m * n < ((int64_t)1 << 31)) {
-        VX_TRY(qmm_fast(x, qweight, scales, biases, y, nullptr, m, n, k, dtype, 0, dtype, dtype,
-                        VX_EPI_STORE, nullptr, 0, st));
-        if (bias) {
-            const int64_t tot = m * n;
-            if (dtype == VX_BF16)
-                hipLaunchKernelGGL(add_bias_kernel<VX_BF16>, dim3((unsigned)vx_cdiv(tot, 256)), dim3(256), 0, st, y, bias, m, n);
-            else
-                hipLaunchKernelGGL(add_bias_kernel<VX_F16>, dim3((unsigned)vx_cdiv(tot, 256)), dim3(256), 0, st, y, bias, m, n);
-            VX_HIP(hipGetLastError());
-        }
-        return 0;
+        // the bias joins the f32 accumulator before the one rounding to T
+        return qmm_fast(x, qweight, scales, biases, y, nullptr, m, n, k, dtype, 0, dtype, dtype, VX_EPI_STORE,
+                        nullptr, 0, st, bias);
     }
     const int64_t tot = m * n;
     dim3 grid((unsigned)vx_cdiv(tot, 256));

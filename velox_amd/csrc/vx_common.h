@@ -15,6 +15,10 @@
 namespace vx {
 int set_error(const std::string &msg);
 int hip_error(hipError_t e, const char *what);
+// A token tree of r nodes (1..64): node 0 is the root (parents[0] < 0) and
+// every other node's parent precedes it (0 <= parents[j] < j), so the tree
+// has no cycle and every ancestor walk ends at the root.
+int check_tree_parents(const int32_t *parents, int64_t r, const char *who);
 }  // namespace vx
 
 #define VX_HIP(call)                                            \

@@ -10,7 +10,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import synth
-from ._lib import (F16, LayerHost, QLinearHost, QwenConfig, RoundOutcome, SeqSlice, StepProfile,
+from ._lib import (F16, LayerHost, QLinearHost, QwenConfig, RoundOutcome, RoundTrace, SeqSlice, StepProfile,
                    VeloxError, WeightsHost, check, lib)
 
 
@@ -106,6 +106,12 @@ class PagedQwen3:
 
     def _run(self, pages, input_ids, seqs, all_rows, tree_parents, stream):
         import torch
+
+        if tree_parents is not None:
+            for nt, _, _ in seqs:
+                if nt != len(tree_parents):
+                    raise VeloxError(f"forward: a tree of {len(tree_parents)} nodes needs new_tokens == "
+                                     f"{len(tree_parents)} in every sequence (got {nt})")
 
         ids = np.ascontiguousarray(input_ids, np.uint32)
         sl = (SeqSlice * len(seqs))()
@@ -214,6 +220,35 @@ class SpecEngine:
         check(lib.vx_spec_last_trace(self._h, cand.ctypes.data_as(C.POINTER(C.c_uint32)),
                                      logits.ctypes.data_as(C.POINTER(C.c_float))))
         return cand, logits
+
+    def set_tracing(self, enable: bool):
+        """Keep every draft step's logits so last_round() can return them."""
+        check(lib.vx_spec_set_tracing(self._h, 1 if enable else 0))
+
+    def last_round(self) -> dict | None:
+        """Everything the last step decided on: state ids, the Philox counter
+        words (stream, round) of its uniforms, the candidates, the verify and
+        draft logits (as f32 copies of the bf16 device values) and the
+        uniforms.  None before the first step."""
+        info = RoundTrace()
+        check(lib.vx_spec_last_trace_info(self._h, C.byref(info), None, None, None))
+        if info.serial == 0:
+            return None
+        n, k, v = info.n, info.draft_k, info.vocab
+        ids = np.zeros(n, np.int64)
+        streams = np.zeros(n, np.uint32)
+        rounds = np.zeros(n, np.uint32)
+        check(lib.vx_spec_last_trace_info(self._h, C.byref(info), ids.ctypes.data_as(C.POINTER(C.c_int64)),
+                                          streams.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                          rounds.ctypes.data_as(C.POINTER(C.c_uint32))))
+        cand, logits = self.last_trace(n, k)
+        uni = np.zeros((n, k + 1, 4), np.float32)
+        dl = np.zeros((n, k, v), np.float32) if info.has_draft_logits else None
+        check(lib.vx_spec_last_trace_draft(self._h, None if dl is None else dl.ctypes.data_as(C.POINTER(C.c_float)),
+                                           uni.ctypes.data_as(C.POINTER(C.c_float))))
+        return {"serial": info.serial, "n": n, "k": k, "temperature": info.temperature, "state_ids": ids,
+                "streams": streams, "rounds": rounds, "candidates": cand, "verify_logits": logits,
+                "draft_logits": dl, "uniforms": uni}
 
     def set_profiling(self, enable: bool):
         check(lib.vx_spec_set_profiling(self._h, 1 if enable else 0))

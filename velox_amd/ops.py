@@ -41,6 +41,17 @@ def _p(t):
     return None if t is None else t.data_ptr()
 
 
+# The reference's index tensors are U32; torch carries the same 32-bit words
+# as int32 (its uint32 has few kernels), so both are accepted.
+_U32 = (torch.int32, torch.uint32)
+
+
+def _u32(msg: str, *ts) -> None:
+    for t in ts:
+        if t is not None and t.dtype not in _U32:
+            raise VeloxError(msg)
+
+
 def qmm_4bit(x, qweight, scales, biases, bias=None, group_size=64):
     """qmm_4bit (metal_kernels.rs:2069-2076): Y[M,N] = X . deq(W)^T (+ bias)."""
     _need(x.dim() == 2 and qweight.dim() == 2, "qmm_4bit: x and qweight must be 2-D")
@@ -119,7 +130,11 @@ def paged_prefill_attention(q, k_pool, v_pool, block_table, cu_seqlens, seq_id_p
           f"seq_id_per_q={seq_id_per_q.shape[0]}, kv_offsets={kv_offsets.shape[0]})")
     _need(k_pool.dtype == q.dtype and v_pool.dtype == q.dtype, "prefill: Q/K/V dtype mismatch")
     _contig("prefill", q=q, k_pool=k_pool, v_pool=v_pool, block_table=block_table, cu_seqlens=cu_seqlens,
-            seq_id_per_q=seq_id_per_q, kv_offsets=kv_offsets)
+            seq_id_per_q=seq_id_per_q, kv_offsets=kv_offsets, tree_mask=tree_mask)
+    _u32("prefill: index tensors must be U32", block_table, cu_seqlens, seq_id_per_q, kv_offsets)
+    if tree_mask is not None:
+        _need(tree_mask.dtype in (torch.int64, torch.uint64) and tuple(tree_mask.shape) == (total_q,),
+              "prefill: tree_mask must be a 64-bit [total_q] tensor")
     out = torch.zeros_like(q)
     check(lib.vx_paged_attention(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_table.data_ptr(),
                                  cu_seqlens.data_ptr(), seq_id_per_q.data_ptr(), kv_offsets.data_ptr(),
@@ -140,6 +155,9 @@ def paged_decode_attention(q, k_pool, v_pool, block_table, kv_lens, scale, slidi
     n_bt, max_blocks = block_table.shape
     _need(n_bt == n, f"paged_decode_attention: block_table N={n_bt} mismatches Q N={n}")
     _need(kv_lens.shape[0] == n, f"paged_decode_attention: kv_lens N={kv_lens.shape[0]} mismatches Q N={n}")
+    _need(k_pool.dtype == q.dtype and v_pool.dtype == q.dtype, "paged_decode_attention: Q/K/V dtype mismatch")
+    _u32("paged_decode_attention: block_table and kv_lens must be U32", block_table, kv_lens)
+    _contig("paged_decode_attention", q=q, k_pool=k_pool, v_pool=v_pool, block_table=block_table, kv_lens=kv_lens)
     out = torch.zeros_like(q)
     check(lib.vx_paged_decode_attention(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
                                         block_table.data_ptr(), kv_lens.data_ptr(), out.data_ptr(), n,
@@ -156,6 +174,7 @@ def batched_rope_decode(x, cos, sin, offsets):
           f"batched_rope_decode: cos/sin shape [Lmax, {half}] mismatches D={d}")
     _need(offsets.shape[0] == n, f"batched_rope_decode: offsets N={offsets.shape[0]} mismatches X N={n}")
     _need(cos.dtype == x.dtype and sin.dtype == x.dtype, "batched_rope_decode: cos/sin dtype must match X")
+    _u32("batched_rope_decode: offsets must be U32", offsets)
     _contig("batched_rope_decode", x=x, cos=cos, sin=sin, offsets=offsets)
     check(lib.vx_rope_inplace(x.data_ptr(), cos.data_ptr(), sin.data_ptr(), offsets.data_ptr(), n, h, d, lmax,
                               _dt(x, "batched_rope_decode"), _stream()))
@@ -168,6 +187,7 @@ def batched_scatter(pool, values, page_ids, slots):
     _need(vh == h and vd == d, f"batched_scatter: values [{n},{vh},{vd}] mismatches pool [_,{h},_,{d}]")
     _need(page_ids.shape[0] == n and slots.shape[0] == n, "batched_scatter: page_ids/slots N mismatches values N")
     _need(pool.dtype == values.dtype, "batched_scatter: pool/values dtype mismatch")
+    _u32("batched_scatter: page_ids and slots must be U32", page_ids, slots)
     _contig("batched_scatter", pool=pool, values=values, page_ids=page_ids, slots=slots)
     check(lib.vx_kv_scatter(pool.data_ptr(), values.data_ptr(), page_ids.data_ptr(), slots.data_ptr(), n, p, h,
                             s, d, _dt(pool, "batched_scatter"), _stream()))
@@ -175,6 +195,7 @@ def batched_scatter(pool, values, page_ids, slots):
 
 # ------------------------------------------------------------------ acceptance
 def argmax_rows(logits):
+    _contig("argmax", logits=logits)
     rows, vocab = logits.shape
     out = torch.zeros(rows, dtype=torch.int32, device=logits.device)
     check(lib.vx_argmax_rows(logits.data_ptr(), out.data_ptr(), rows, vocab, _dt(logits, "argmax"), _stream()))
@@ -184,6 +205,9 @@ def argmax_rows(logits):
 def accept_greedy(logits, candidates):
     """logits [B, k+1, V]; candidates [B, k] -> (accepted [B], tokens [B, k+1])."""
     b, r, v = logits.shape
+    _need(tuple(candidates.shape) == (b, r - 1), "accept_greedy: candidates must be [B, k]")
+    _u32("accept_greedy: candidates must be U32", candidates)
+    _contig("accept_greedy", logits=logits, candidates=candidates)
     acc = torch.zeros(b, dtype=torch.int32, device=logits.device)
     tok = torch.zeros((b, r), dtype=torch.int32, device=logits.device)
     check(lib.vx_accept_greedy(logits.data_ptr(), candidates.data_ptr(), acc.data_ptr(), tok.data_ptr(), b,
@@ -193,6 +217,14 @@ def accept_greedy(logits, candidates):
 
 def accept_stochastic(target_logits, draft_logits, candidates, uniforms, temperature):
     b, r, v = target_logits.shape
+    _need(tuple(draft_logits.shape) == (b, r - 1, v) and draft_logits.dtype == target_logits.dtype,
+          "accept_stochastic: draft logits must be [B, k, V] in the target's dtype")
+    _need(tuple(candidates.shape) == (b, r - 1), "accept_stochastic: candidates must be [B, k]")
+    _need(uniforms.dtype == torch.float32 and tuple(uniforms.shape) == (b, r, 4),
+          "accept_stochastic: uniforms must be f32 [B, k+1, 4]")
+    _u32("accept_stochastic: candidates must be U32", candidates)
+    _contig("accept_stochastic", target_logits=target_logits, draft_logits=draft_logits, candidates=candidates,
+            uniforms=uniforms)
     acc = torch.zeros(b, dtype=torch.int32, device=target_logits.device)
     tok = torch.zeros((b, r), dtype=torch.int32, device=target_logits.device)
     check(lib.vx_accept_stochastic(target_logits.data_ptr(), draft_logits.data_ptr(), candidates.data_ptr(),
@@ -203,6 +235,9 @@ def accept_stochastic(target_logits, draft_logits, candidates, uniforms, tempera
 
 def sample_rows(logits, uniforms, temperature, uniform_stride=1):
     rows, v = logits.shape
+    _need(uniforms.dtype == torch.float32 and uniforms.numel() >= (rows - 1) * uniform_stride + 1,
+          "sample: uniforms must be f32 with one value per row")
+    _contig("sample", logits=logits, uniforms=uniforms)
     out = torch.zeros(rows, dtype=torch.int32, device=logits.device)
     check(lib.vx_sample_rows(logits.data_ptr(), uniforms.data_ptr(), uniform_stride, out.data_ptr(), rows, v,
                              temperature, _dt(logits, "sample"), None, 0, _stream()))
@@ -218,6 +253,7 @@ def kv_compact_path(pages, block_tables, kv_offsets, accepted, path):
     b, mb = block_tables.shape
     _need(path.dim() == 2 and path.shape[0] == b and accepted.shape[0] == b and kv_offsets.shape[0] == b,
           "kv_compact_path: shape mismatch")
+    _u32("kv_compact_path: index tensors must be 32-bit", block_tables, kv_offsets, accepted, path)
     _contig("kv_compact_path", block_tables=block_tables, kv_offsets=kv_offsets, accepted=accepted, path=path)
     check(lib.vx_kv_compact_path(pages._h, block_tables.data_ptr(), mb, kv_offsets.data_ptr(), accepted.data_ptr(),
                                  path.data_ptr(), b, path.shape[1], _stream()))
@@ -228,6 +264,10 @@ def accept_tree(logits, parents, node_tokens):
     import ctypes as C
 
     b, r, v = logits.shape
+    _need(len(parents) == r, f"accept_tree: {len(parents)} parents for {r} nodes")
+    _need(tuple(node_tokens.shape) == (b, r), "accept_tree: node_tokens must be [B, R]")
+    _u32("accept_tree: node_tokens must be U32", node_tokens)
+    _contig("accept_tree", logits=logits, node_tokens=node_tokens)
     par = (C.c_int32 * r)(*[int(x) for x in parents])
     acc = torch.zeros(b, dtype=torch.int32, device=logits.device)
     path = torch.zeros((b, r), dtype=torch.int32, device=logits.device)
