@@ -106,7 +106,15 @@ def test_forward_tree_matches_oracle(cuda):
     assert_allclose_elementwise("tree verify logits", got, ref, 1e-2, 1e-2)
 
 
-def run_lockstep(cfg, w, draft_layers, prompts, k, rounds, temperature=0.0, seed=0, ps=16):
+# Zero-mean int4 biases put the logits at |logit| ~ 1 instead of the
+# benchmark's ~200, where the bf16 model's own rounding noise exceeds the
+# north_star's absolute 1e-2: on the tiny model the oracle's bf16 logits
+# differ from an f32-activation oracle by up to 0.047 at the first draft
+# step (10 % of them by more than 1e-2 + 1e-2|ref|), and the gap grows with
+# the context.  Those stress runs therefore measure that noise on every
+# compared forward (Lockstep noise_ref) and allow the GPU twice of it, never
+# less than the north_star bound; every decision stays bit-exact.
+def run_lockstep(cfg, w, draft_layers, prompts, k, rounds, temperature=0.0, seed=0, ps=16, noise_ref=False):
     """GPU engine rounds, each replayed and checked by the oracle mirror
     (tests/lockstep.py); returns the accepted counts of every round."""
     from velox_amd import engine
@@ -123,7 +131,8 @@ def run_lockstep(cfg, w, draft_layers, prompts, k, rounds, temperature=0.0, seed
                            sample_seed=seed)
     ge.set_tracing(True)
     gs = ge.prefill_batch(prompts)
-    ls = Lockstep(cfg, w, draft_layers, max_tokens, len(prompts), ps=ps, temperature=temperature, seed=seed)
+    ls = Lockstep(cfg, w, draft_layers, max_tokens, len(prompts), ps=ps, temperature=temperature, seed=seed,
+                  noise_ref=noise_ref)
     ls.prefill(prompts)
     accepted = []
     for r in range(rounds):
@@ -162,7 +171,7 @@ def test_spec_greedy_lockstep(cuda, weights):
         w = zero_mean(w)
     rng = np.random.default_rng(7)
     prompts = [rng.integers(0, cfg["vocab"], size=L).astype(np.uint32) for L in (5, 9, 17)]
-    acc = run_lockstep(cfg, w, 2, prompts, k=4, rounds=6)
+    acc = run_lockstep(cfg, w, 2, prompts, k=4, rounds=6, noise_ref=weights == "zero_mean")
     if weights == "zero_mean":
         assert min(acc) < 4, "no round rejected a candidate"
 
@@ -179,7 +188,7 @@ def test_spec_stochastic_lockstep(cuda, temperature, k):
     w = zero_mean(synth.host_weights(cfg, 6))
     rng = np.random.default_rng(11)
     prompts = [rng.integers(0, cfg["vocab"], size=L).astype(np.uint32) for L in (6, 11, 4)]
-    acc = run_lockstep(cfg, w, 2, prompts, k=k, rounds=5, temperature=temperature, seed=1234)
+    acc = run_lockstep(cfg, w, 2, prompts, k=k, rounds=5, temperature=temperature, seed=1234, noise_ref=True)
     assert min(acc) < k, "every candidate accepted: the residual draw never ran"
 
 

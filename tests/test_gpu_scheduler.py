@@ -111,8 +111,10 @@ def test_scheduler_stochastic_lockstep(cuda):
     new = 12
     s = BatchScheduler(e, (), SchedulerConfig(max_batch_tokens=48, prefix_cache_capacity=32, draft_k=4))
     ids = [s.submit(p, new, temperature=0.7) for p in prompts]
+    # zero-mean weights: logits at |logit| ~ 1, compared against the bf16
+    # model's own measured rounding noise (see test_gpu_engine.run_lockstep)
     ls = Lockstep(cfg, w, 2, max(len(p) for p in prompts) + new + 12, len(prompts), temperature=0.7, seed=5,
-                  fix_hole=True)
+                  fix_hole=True, noise_ref=True)
     ls.prefill(prompts, streams=ids)
     index_of = {rid: i for i, rid in enumerate(ids)}
     serial, steps = 0, 0

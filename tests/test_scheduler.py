@@ -387,3 +387,38 @@ def test_temperatures_run_in_separate_rounds_with_request_streams():
     assert sorted(v[0] for v in seen.values()) == ids  # stream = request id
     assert {round(v[1], 3) for v in seen.values()} == {0.0, 0.7}
     assert not eng.errors
+
+
+def test_owner_destruction_closes_the_scheduler_first():
+    """Destroying a scheduler frees its live states through the engine, so an
+    engine (or page pool) that goes first must close the schedulers bound to
+    it: velox_amd.engine.close_dependents, which SpecEngine and PagedKvCache
+    call before destroying themselves (Python finalises one garbage cycle,
+    and whatever is left at exit, in no set order)."""
+    import gc
+
+    from velox_amd.engine import close_dependents
+
+    class OwnedToy(ToyEngine):
+        def __init__(self):
+            super().__init__()
+            self._dependents = []
+
+    eng = OwnedToy()
+    s = BatchScheduler(eng, (), SchedulerConfig(max_batch_tokens=512, prefix_cache_capacity=0, draft_k=4))
+    assert eng._dependents == [s]
+    s.submit(prompt(5, 20), 30)
+    s.step()
+    s.step()
+    assert eng.states, "the request holds a live state"
+    close_dependents(eng)  # what the owner's __del__ runs first
+    assert s._h is None and not eng.states and eng.free_pages() == [64, 64]
+    assert eng._dependents == []
+    s.close()  # closing again is a no-op
+    # a scheduler and its engine that die together in one cycle, in either order
+    eng2 = OwnedToy()
+    s2 = BatchScheduler(eng2, (), SchedulerConfig(prefix_cache_capacity=0, draft_k=4))
+    s2.submit(prompt(6, 9), 5)
+    s2.step()
+    del s2, eng2
+    gc.collect()

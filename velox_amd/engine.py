@@ -19,6 +19,7 @@ class PagedKvCache:
     device), LIFO free list (page 0 first), refcounts, all-or-nothing alloc."""
 
     def __init__(self, num_layers, num_kv_heads, head_dim, page_size, num_pages, dtype=F16):
+        self._dependents = []  # native objects that touch these pools when destroyed
         h = C.c_void_p()
         check(lib.vx_pages_create(num_layers, num_kv_heads, head_dim, page_size, num_pages, dtype,
                                   C.byref(h)))
@@ -55,6 +56,7 @@ class PagedKvCache:
         return lib.vx_pages_pool(self._h, layer, kv)
 
     def __del__(self, _destroy=lib.vx_pages_destroy):  # bound now: module globals may be gone at exit
+        close_dependents(self)
         if getattr(self, "_h", None):
             _destroy(self._h)
             self._h = None
@@ -146,6 +148,16 @@ class PagedQwen3:
             self._h = None
 
 
+def close_dependents(owner) -> None:
+    """Close the native objects whose destruction reaches into `owner` (a
+    scheduler frees its states' pages through the engine) before `owner`
+    itself goes.  Python finalises objects of one garbage cycle in no set
+    order (PEP 442), and at interpreter exit whatever is left goes that way,
+    so the owner closes them first; a closed dependent is a no-op."""
+    for d in list(getattr(owner, "_dependents", ())):
+        d.close()
+
+
 @dataclass
 class RoundOutcome_:
     committed_tokens: list
@@ -177,6 +189,7 @@ class SpecEngine:
 
     def __init__(self, target: PagedQwen3, target_pages: PagedKvCache, draft: PagedQwen3,
                  draft_pages: PagedKvCache, temperature=0.0, sample_seed=0, fix_draft_hole=False):
+        self._dependents = []
         h = C.c_void_p()
         check(lib.vx_spec_create(target._h, target_pages._h, draft._h, draft_pages._h, temperature, sample_seed,
                                  1 if fix_draft_hole else 0, C.byref(h)))
@@ -269,6 +282,7 @@ class SpecEngine:
         lib.vx_spec_free(self._h, state.id)
 
     def __del__(self, _destroy=lib.vx_spec_destroy):  # bound now: module globals may be gone at exit
+        close_dependents(self)
         if getattr(self, "_h", None):
             _destroy(self._h)
             self._h = None

@@ -75,6 +75,11 @@ class BatchScheduler:
             check(lib.vx_sched_create(engine._h, C.byref(c), eos, len(eos_token_ids), stream, C.byref(h)))
         self._h = h
         self._engine = engine  # the engine must outlive the scheduler
+        # destroying the scheduler frees its states through the engine and
+        # the engine's page pools: they close it before they go
+        self._owners = [o for o in (engine, *getattr(engine, "_refs", ())) if hasattr(o, "_dependents")]
+        for o in self._owners:
+            o._dependents.append(self)
 
     def submit(self, prompt_tokens, max_tokens: int, temperature: float = 0.0, stream: int | None = None) -> int:
         """scheduler.rs:147-185; returns the request id."""
@@ -133,6 +138,10 @@ class BatchScheduler:
         if getattr(self, "_h", None):
             _destroy(self._h)
             self._h = None
+        for o in getattr(self, "_owners", ()):
+            if self in o._dependents:
+                o._dependents.remove(self)
+        self._owners = []
 
     def __del__(self):
         self.close()
