@@ -43,6 +43,20 @@ int vx_qmm_4bit(const void *x, const uint32_t *qweight, const void *scales, cons
                 const void *bias, void *y, int64_t m, int64_t n, int64_t k, int64_t group_size,
                 int dtype, void *stream);
 
+/* vx_qmm_4bit for callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  No
+ * counterpart in the reference.  Same arguments, validation, kernel plan and
+ * results (bit for bit) as vx_qmm_4bit; it calls no hipMalloc / hipFree and
+ * no allocating library routine.  Its split-K partials go to a static device
+ * array of VX_QMM_NOALLOC_SCRATCH_BYTES per GPU (held until the process
+ * ends); a shape whose plan needs more returns an error naming the sizes.
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (e.g. on two streams) race. */
+#define VX_QMM_NOALLOC_SCRATCH_BYTES ((size_t)(16u << 20) + 65536u)
+int vx_qmm_4bit_noalloc(const void *x, const uint32_t *qweight, const void *scales, const void *biases,
+                        const void *bias, void *y, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                        int dtype, void *stream);
+
 /* Epilogue variants used by the fused verify forward. */
 typedef enum {
     VX_EPI_STORE = 0,    /* Y = round_T(acc)                                   */

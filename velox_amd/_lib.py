@@ -120,6 +120,7 @@ _SIGS = {
     "vx_last_error": (C.c_char_p, []),
     "vx_version": (C.c_char_p, []),
     "vx_qmm_4bit": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]),
+    "vx_qmm_4bit_noalloc": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]),
     "vx_qmm_4bit_ex": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i32, i32, i32, i32, vp,
                              C.c_size_t, vp]),
     "vx_qmm_workspace_size": (C.c_size_t, [i64, i64, i64]),

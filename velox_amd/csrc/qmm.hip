@@ -32,6 +32,9 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 #include "vx_common.h"
@@ -1941,6 +1944,63 @@ extern "C" int vx_qmm_4bit_ex(const void *x, const uint32_t *qweight, const void
     VX_REQUIRE(fast_ok(VX_F16, k, group_size, x, qweight, scales, biases), "qmm_4bit_ex: misaligned operand");
     return qmm_fast(x, qweight, scales, biases, y, residual, m, n, k, VX_F16, x_shift, round_dtype,
                     y_dtype, epilogue, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// vx_qmm_4bit without allocation.  Its split-K partials live in `scratch`, a
+// static device array laid out like a caller workspace (the reserved head,
+// then the partials); each GPU holds its own copy until the process ends.
+// Kernel arguments take the array's device address from hipGetSymbolAddress,
+// resolved once per device on the first call there (the array's name is a
+// host-side stand-in, never a device address).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kNoAllocScratchBytes = VX_QMM_NOALLOC_SCRATCH_BYTES;
+static_assert(kNoAllocScratchBytes > kCounterBytes, "the scratch holds the workspace head and the partials");
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+int scratch_address(void **out) {
+    static std::mutex mu;
+    static std::map<int, void *> per_device;
+    int dev = 0;
+    VX_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = per_device.find(dev);
+    if (it == per_device.end()) {
+        void *p = nullptr;
+        VX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        VX_REQUIRE(p != nullptr, "qmm_4bit_noalloc: no device address for the static scratch");
+        it = per_device.emplace(dev, p).first;
+    }
+    *out = it->second;
+    return 0;
+}
+}  // namespace
+
+extern "C" int vx_qmm_4bit_noalloc(const void *x, const uint32_t *qweight, const void *scales,
+                                   const void *biases, const void *bias, void *y, int64_t m, int64_t n,
+                                   int64_t k, int64_t group_size, int dtype, void *stream) {
+    // same validation and path choice as vx_qmm_4bit
+    VX_REQUIRE(k % 8 == 0, "qmm_4bit: K must be a multiple of 8");
+    VX_REQUIRE(group_size != 0 && group_size % 8 == 0 && k % group_size == 0,
+               "qmm_4bit: group_size must be a multiple of 8 and divide K");
+    VX_REQUIRE(dtype == VX_F32 || dtype == VX_F16 || dtype == VX_BF16, "qmm_4bit: unsupported dtype");
+    VX_REQUIRE(m >= 0 && n >= 0, "qmm_4bit: negative shape");
+    if (m == 0 || n == 0) return 0;
+    VX_REQUIRE(x && qweight && scales && biases && y, "qmm_4bit: null tensor");
+    const bool fast = dtype != VX_F32 && fast_ok(dtype, k, group_size, x, qweight, scales, biases) &&
+                      m * n < ((int64_t)1 << 31);
+    if (!fast)  // the one-thread-per-output kernel needs no scratch
+        return vx_qmm_4bit(x, qweight, scales, biases, bias, y, m, n, k, group_size, dtype, stream);
+    const size_t need = kCounterBytes + make_plan(m, n, k, VX_EPI_STORE, dtype == VX_F16).partial_bytes;
+    if (need > kNoAllocScratchBytes)
+        return set_error("qmm_4bit_noalloc: this shape's split-K partials need " + std::to_string(need) +
+                         " bytes, above the static scratch of " + std::to_string(kNoAllocScratchBytes) +
+                         " bytes (use vx_qmm_4bit_ex with a workspace)");
+    void *ws = nullptr;
+    VX_TRY(scratch_address(&ws));
+    return qmm_fast(x, qweight, scales, biases, y, nullptr, m, n, k, dtype, 0, dtype, dtype, VX_EPI_STORE, ws,
+                    kNoAllocScratchBytes, (hipStream_t)stream, bias);
 }
 
 extern "C" size_t vx_qmm_workspace_size(int64_t m, int64_t n, int64_t k) {
