@@ -45,48 +45,94 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg, weights, batch, k, threads):
+def host_cpu():
+    """Host cores this process may run on, and the CPU model."""
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cores, model
+
+
+def snapshot_kv(engine_obj, states, target_pages, draft_pages):
+    """Host copies of the KV pages the states hold after the GPU prefill:
+    {(which, layer, kv): (block table, f16 pages [n, h_kv, ps, d])}."""
+    import ctypes as C
+
+    from velox_amd._lib import lib
+
+    rt = C.CDLL("libamdhip64.so.7")
+    rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    snap = []
+    for which, pg in ((0, target_pages), (1, draft_pages)):
+        shape = (pg.num_pages, pg.num_kv_heads, pg.page_size, pg.head_dim)
+        tables = []
+        for s in states:
+            n = lib.vx_spec_state_pages(engine_obj._h, s.id, which, None, 0)
+            buf = (C.c_uint32 * n)()
+            lib.vx_spec_state_pages(engine_obj._h, s.id, which, buf, n)
+            tables.append(np.array(buf[:n], np.uint32))
+        used = np.unique(np.concatenate(tables))
+        for layer in range(pg.num_layers):
+            for kv in (0, 1):
+                pool = np.empty(shape, np.float16)
+                assert rt.hipMemcpy(pool.ctypes.data, pg.layer_pool_ptr(layer, kv), pool.nbytes, 2) == 0
+                snap.append((which, layer, kv, tables, {int(u): pool[u].copy() for u in used}))
+    return snap
+
+
+def cpu_baseline(cfg, weights, prompts, k, kv_snapshot, rounds=2):
     """The oracle (the reference's algorithm restated in C: qmm_4bit_cpu loop
-    order, OpenMP over output features) on the same workload, bounded sample:
-    one real speculative round at batch 16 with the full 4-layer draft and the
-    target truncated to 2 layers, plus one timed 80-row target decoder layer
-    (its five int4 GEMMs, >98% of a layer's CPU time at this context); the
-    full-model round time is T(2-layer round) + 34 * T(layer)."""
+    order, OpenMP over output features) running the same spec rounds on the
+    host: full Qwen3-4B-shape target, 4-layer draft, batch 16, k = 4, greedy,
+    the same 128-token prompts.  The oracle's states take the KV pages of the
+    GPU prefill (copied, not timed: a 16 x 127-row prefill through 36 layers
+    is far beyond a bounded CPU sample); one warm-up round, then `rounds`
+    timed full rounds at the GPU run's context."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import vxo
 
     from velox_amd import synth
 
+    cores, model = host_cpu()
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     wt = synth.as_model_dtype(weights, "bf16")
     ocfg = dict(cfg, dtype=vxo.BF16)
-    t = vxo.Model(ocfg, wt, n_layers=2, threads=threads)
-    d = vxo.Model(ocfg, wt, n_layers=4, threads=threads)
-    HK, D = cfg["n_kv_heads"], cfg["head_dim"]
-    e = vxo.SpecEngine(t, vxo.Pages(2, HK, D, 16, batch * 2), d, vxo.Pages(4, HK, D, 16, batch * 2))
-    prompts = [synth.prompt(0, 4, cfg["vocab"], stream=b) for b in range(batch)]
-    st = e.prefill(prompts)
-    log("[cpu] oracle prefill done; timing one round (2-layer target, 4-layer draft)")
+    B, L, HK, D = len(prompts), cfg["layers"], cfg["n_kv_heads"], cfg["head_dim"]
+    t = vxo.Model(ocfg, wt, threads=cores)
+    d = vxo.Model(ocfg, wt, n_layers=4, threads=cores)
+    del wt
+    npg = B * ((len(prompts[0]) + (rounds + 2) * (k + 1) + 15) // 16 + 1)
+    tp, dp = vxo.Pages(L, HK, D, 16, npg), vxo.Pages(4, HK, D, 16, npg)
+    e = vxo.SpecEngine(t, tp, d, dp)
+    st = e.adopt(prompts)
+    for which, layer, kv, tables, pages in kv_snapshot:
+        pool = (tp if which == 0 else dp).pool(layer, kv)
+        for b in range(B):
+            ob = st[b].target_blocks if which == 0 else st[b].draft_blocks
+            for i, gpage in enumerate(tables[b]):
+                pool[ob[i]] = pages[int(gpage)].astype(np.float32)
+    log(f"[cpu] oracle states adopted with the GPU prefill's KV; warm-up round ({cores} threads)")
+    e.step(st, k)
     t0 = time.perf_counter()
-    out = e.step(st, k)
-    t_round2 = time.perf_counter() - t0
-    committed = int(sum(len(c) for c in out["committed"]))
-    log(f"[cpu] 2-layer round {t_round2:.2f}s; timing one 80-row decoder layer")
-    rows = batch * (k + 1)
-    x = vxo.round_to(np.random.default_rng(0).standard_normal((rows, cfg["hidden"])).astype(np.float32), vxo.BF16)
-    xf = vxo.round_to(np.random.default_rng(1).standard_normal((rows, cfg["inter"])).astype(np.float32), vxo.BF16)
-    xo = vxo.round_to(np.random.default_rng(2).standard_normal((rows, cfg["n_heads"] * D)).astype(np.float32), vxo.BF16)
-    t1 = time.perf_counter()
-    for name, inp in (("q", x), ("k", x), ("v", x), ("o", xo), ("gate", x), ("up", x), ("down", xf)):
-        p = f"layers.2.{name}"
-        vxo.qmm_4bit(inp, wt[p + ".qweight"], wt[p + ".scales"], wt[p + ".biases"], None, 64, threads)
-    t_layer = time.perf_counter() - t1
-    t_full = t_round2 + (cfg["layers"] - 2) * t_layer
-    log(f"[cpu] layer {t_layer:.2f}s -> full round estimate {t_full:.1f}s")
-    return {"value": committed / t_full, "unit": "accepted tok/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle spec loop (oracle/vxo.c, OpenMP {threads} threads), Qwen3-4B shape, batch {batch}, "
-                       f"k={k}, greedy, 4-token prompts: one measured round with the target truncated to 2 layers "
-                       f"({t_round2:.2f} s, {committed} tokens) + 34 x one measured 80-row decoder layer "
-                       f"({t_layer:.2f} s) = {t_full:.1f} s per full round")}
+    committed = 0
+    for _ in range(rounds):
+        out = e.step(st, k)
+        committed += int(sum(len(c) for c in out["committed"]))
+    dt = time.perf_counter() - t0
+    log(f"[cpu] {rounds} full rounds in {dt:.2f}s, {committed} tokens")
+    return {"value": committed / dt, "unit": "accepted tok/s", "cores": cores, "kind": "port",
+            "sample": (f"oracle spec loop (oracle/vxo.c restating spec.rs / qwen3.rs / metal_kernels.rs CPU refs, "
+                       f"OpenMP {cores} threads on {model}, nproc {os.cpu_count()}): {rounds} timed full rounds "
+                       f"(36-layer target, 4-layer draft, batch {B}, k={k}, greedy, 128-token prompts) after one "
+                       f"warm-up round, from states holding the GPU prefill's KV pages; {dt:.2f} s, "
+                       f"{committed} tokens")}
 
 
 def traffic_per_op():
@@ -121,7 +167,7 @@ def run_spec(args):
     target = engine.PagedQwen3(cfg, w)
     draft = engine.PagedQwen3(cfg, w, n_layers=4)
     log(f"[bench] models on device ({time.time() - t0:.1f}s)")
-    rounds = args.warmup + args.steps + args.profile_steps
+    rounds = args.warmup + args.steps + 2 * args.profile_steps
     max_len = args.prompt + (rounds + 1) * (k + 1) + 16
     pages_per_seq = (max_len + 15) // 16 + 1
     HK, D = cfg["n_kv_heads"], cfg["head_dim"]
@@ -133,6 +179,7 @@ def run_spec(args):
     states = e.prefill_batch(prompts)
     torch.cuda.synchronize()
     log(f"[bench] prefill {B}x{args.prompt} in {time.time() - t1:.1f}s")
+    kv_snapshot = None if args.no_cpu_baseline else snapshot_kv(e, states, tp, dp)
     for i in range(args.warmup):
         e.step_batch(states, k)
     torch.cuda.synchronize()
@@ -148,6 +195,25 @@ def run_spec(args):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - ts
     log(f"[bench] timed {args.steps} rounds: {elapsed * 1e3:.1f} ms, {committed} tokens")
+    # outside the timed region: the last round's decisions, re-derived from
+    # its own verify logits (argmax_slice: first index of the maximum)
+    cand, vlog = e.last_trace(B, k)
+    decisions_ok = True
+    for b in range(B):
+        am = vlog[b].argmax(axis=1)
+        a = 0
+        while a < k and cand[b, a] == am[a]:
+            a += 1
+        want = list(cand[b, :a]) + [am[a]]
+        decisions_ok &= outs[b].accepted == a and list(outs[b].committed_tokens) == [int(x) for x in want]
+    log(f"[bench] last round's accept decisions re-derived from its logits: {'ok' if decisions_ok else 'MISMATCH'}")
+    # undisturbed phase times (events at the draft / verify / accept boundaries only)
+    e.set_profiling(True, phases_only=True)
+    phases = []
+    for i in range(args.profile_steps):
+        e.step_batch(states, k)
+        phases.append(e.last_profile())
+    e.set_profiling(False)
     # profiled rounds (HIP events on the engine stream around every kernel)
     e.set_profiling(True)
     profs = []
@@ -206,12 +272,20 @@ def run_spec(args):
                      agg["verify_qmm_ms"] * 1e3 / max(1, agg["verify_qmm_launches"]),
                      "algorithmic_bytes_per_launch": None if agg is None else
                      agg["verify_qmm_bytes"] / max(1, agg["verify_qmm_launches"])},
-        "kernel_breakdown_ms": None if agg is None else {kk: v for kk, v in agg.items() if kk.endswith("_ms")},
+        "ms_per_round": elapsed * 1e3 / args.steps,
+        "decisions_check": "ok" if decisions_ok else "mismatch",
+        # phase times of undisturbed rounds (they sum to about ms_per_step;
+        # the commit's host work is the remainder)
+        "kernel_breakdown_ms": None if not phases else {
+            kk: float(np.mean([p[kk] for p in phases])) for kk in ("draft_ms", "verify_ms", "accept_ms")},
+        # per-class sums from the per-kernel event rounds: each event pair also
+        # brackets its kernel's dispatch gap, so these run above the phases
+        "kernel_class_ms_event_bracketed": None if agg is None else {
+            kk: v for kk, v in agg.items() if kk.endswith("_ms") and kk not in ("draft_ms", "verify_ms", "accept_ms")},
     }
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
         t2 = time.time()
-        res["cpu_baseline"] = cpu_baseline(cfg, w, B, k, threads)
+        res["cpu_baseline"] = cpu_baseline(cfg, w, prompts, k, kv_snapshot)
         log(f"[bench] cpu baseline in {time.time() - t2:.1f}s")
     else:
         res["cpu_baseline"] = None
@@ -566,6 +640,41 @@ def run_tree(args):
     print(json.dumps(res), flush=True)
 
 
+def run_gemm(args):
+    """One verify GEMM shape launched back to back on the engine's packed path
+    (cache-rotated weight copies), for counter runs under rocprofv3 --pmc:
+    e.g. --mode gemm --shape gate_up --m 80."""
+    import torch
+
+    from velox_amd import _lib, ops, synth
+
+    torch.cuda.set_device(0)
+    shapes = {"qkv": (6144, 2560), "o": (2560, 4096), "gate_up": (19456, 2560), "down": (2560, 9728),
+              "lm_head": (151936, 2560)}
+    n, kk = shapes[args.shape]
+    lin = synth.qlinear(1, f"bench.{args.shape}", n, kk, 64)
+    W = torch.from_numpy(lin["qweight"].view(np.int32)).cuda()
+    S = torch.from_numpy(lin["scales"]).cuda()
+    Bs = torch.from_numpy(lin["biases"]).cuda()
+    copies = max(2, int(np.ceil(640e6 / (0.5625 * n * kk))))
+    packed = [ops.qmm_pack_4bit(W, S, Bs) for _ in range(copies)]
+    epi = _lib.EPI_SWIGLU if args.shape == "gate_up" else _lib.EPI_STORE
+    x = torch.randn((args.m, kk), dtype=torch.float16, device="cuda")
+    y = torch.empty((args.m, n // 2 if epi == _lib.EPI_SWIGLU else n), dtype=torch.float16, device="cuda")
+    ws = torch.zeros(256 << 20, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.iters):
+        ops.qmm_4bit_packed(x, packed[i % copies], n, y, epilogue=epi, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.iters
+    byt = 0.5625 * n * kk + 2 * args.m * kk + 2 * y.numel()
+    print(json.dumps({"mode": "gemm", "shape": args.shape, "n": n, "k": kk, "m": args.m, "iters": args.iters,
+                      "us_per_launch": us, "algorithmic_bytes": byt, "gbs": byt / (us * 1e-6) / 1e9}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -575,7 +684,11 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=128)
-    ap.add_argument("--mode", choices=["spec", "qmm", "continuous", "tree", "config0"], default="spec")
+    ap.add_argument("--mode", choices=["spec", "qmm", "continuous", "tree", "config0", "gemm"], default="spec")
+    ap.add_argument("--shape", choices=["qkv", "o", "gate_up", "down", "lm_head"], default="gate_up",
+                    help="gemm mode: the verify GEMM shape")
+    ap.add_argument("--m", type=int, default=80, help="gemm mode: rows")
+    ap.add_argument("--iters", type=int, default=200, help="gemm mode: launches")
     ap.add_argument("--batch-tokens", type=int, default=8192, help="continuous mode: max_batch_tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
@@ -585,6 +698,8 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the verify path "
               "shards data-parallel over sequences with no cross-GPU exchange.", file=sys.stderr)
         sys.exit(2)
+    if args.mode == "gemm":
+        return run_gemm(args)
     if args.mode == "qmm":
         run_qmm(args)
     elif args.mode == "continuous":

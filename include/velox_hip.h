@@ -335,6 +335,9 @@ typedef struct {
     double draft_kernel_ms[3], draft_kernel_bytes[3];
     int64_t draft_kernel_launches[3];
 } vx_step_profile;
+/* enable: 0 off; 1 events around every kernel and at the phase boundaries
+ * (each event pair also brackets its kernel's dispatch gap); 2 phase
+ * boundaries only (draft / verify / accept ms of an undisturbed round). */
 int vx_spec_set_profiling(vx_spec *e, int enable);
 int vx_spec_last_profile(const vx_spec *e, vx_step_profile *out);
 

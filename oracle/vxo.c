@@ -947,6 +947,21 @@ int vxo_spec_prefill(vxo_spec *e, const uint32_t *const *prompts, const int64_t 
     return rc;
 }
 
+int vxo_spec_adopt(vxo_spec *e, const uint32_t *prompt, int64_t len, vxo_spec_state *s) {
+    const int64_t ps = e->target_pages->page_size;
+    if (len < 2) return set_err("speculative prefill requires a prompt with at least 2 tokens");
+    memset(s, 0, sizeof *s);
+    const int64_t need = (len - 1 + 1 + ps - 1) / ps;
+    if (grow(e->target_pages, &s->target_blocks, &s->n_target_blocks, need))
+        return set_err("alloc target prefill pages");
+    if (grow(e->draft_pages, &s->draft_blocks, &s->n_draft_blocks, need))
+        return set_err("alloc draft prefill pages");
+    s->kv_len = len - 1;
+    s->last_token = prompt[len - 1];
+    push_tokens(s, prompt, len);
+    return 0;
+}
+
 int vxo_spec_step(vxo_spec *e, vxo_spec_state *st, int64_t n, int64_t d, int64_t eos,
                   int32_t *accepted, uint32_t *committed, int32_t *stop, uint32_t *tr_cand,
                   float *tr_logits) {

@@ -30,7 +30,13 @@
  *   rope_tables / rope_apply  closed form (f32 argument) / complex rotation
  *   kv_scatter                byte-exact copy
  *   argmax, accept_greedy     spec.rs:271-301, :356-366 cases (first index, NaN)
- *   row_softmax_stats, sample_residual, accept_stochastic, sample_draft
+ *   row_softmax_stats         float64 log-sum-exp at V = 151936 with the maximum in
+ *                             the first, a middle, the last and the partial chunk
+ *                             (test_oracle_sampler.py)
+ *   sample_residual           float64 inverse CDF at V = 8193 / 20000 / 151936 with
+ *                             mass on both sides of every 256 / 8192 boundary;
+ *                             chi-square of draws straddling them
+ *   accept_stochastic, sample_draft
  *                             p == q accepts everything; emitted tokens follow p
  *                             (chi-square); no reference counterpart exists
  *   accept_tree, tree_masks   brute-force walks on small trees
@@ -242,6 +248,11 @@ typedef struct {
 /* prefill (spec.rs:131-182) for n prompts, batched into one forward per model. */
 int vxo_spec_prefill(vxo_spec *e, const uint32_t *const *prompts, const int64_t *lens,
                      int64_t n, vxo_spec_state *states);
+/* The state prefill would produce for prompt[0, len) (kv_len = len - 1,
+ * pages for len positions in both pools) without running the models: the
+ * caller fills the KV pages (e.g. copied from another implementation's
+ * prefill of the same prompt) before stepping. */
+int vxo_spec_adopt(vxo_spec *e, const uint32_t *prompt, int64_t len, vxo_spec_state *s);
 /* step (spec.rs:186-316) for n states; committed[b, 0..accepted[b]] written to
  * committed (stride draft_k + 1); stop[b] as spec.rs:306-309 (eos < 0: none).
  * Optional trace outputs (NULL to skip): candidates [n, k],

@@ -70,6 +70,7 @@ def _load() -> C.CDLL:
         "vxo_forward": (C.c_int, [vp, vp, _u32p, vp, _i64, C.c_int, vp, _f32p]),
         "vxo_spec_prefill": (C.c_int, [vp, vp, vp, _i64, vp]),
         "vxo_spec_step": (C.c_int, [vp, vp, _i64, _i64, _i64, _i32p, _u32p, _i32p, vp, vp]),
+        "vxo_spec_adopt": (C.c_int, [vp, _u32p, _i64, vp]),
         "vxo_spec_free": (None, [vp, vp]),
     }
     for name, (res, args) in sig.items():
@@ -419,6 +420,16 @@ class SpecEngine:
         states = (_State * n)()
         _check(lib.vxo_spec_prefill(C.byref(self._s), C.cast(ptrs, C.c_void_p),
                                     lens.ctypes.data_as(C.c_void_p), n, C.cast(states, C.c_void_p)))
+        return states
+
+    def adopt(self, prompts):
+        """States as prefill would leave them, with the KV pages left for the
+        caller to fill (see vxo_spec_adopt)."""
+        n = len(prompts)
+        states = (_State * n)()
+        for b, p in enumerate(prompts):
+            p = np.ascontiguousarray(p, np.uint32)
+            _check(lib.vxo_spec_adopt(C.byref(self._s), p, p.size, C.byref(states[b])))
         return states
 
     def step(self, states, draft_k, eos=-1, trace=False):

@@ -964,7 +964,7 @@ struct vx_spec {
     std::vector<uint32_t> last_streams, last_rounds;
     Prof prof_draft, prof_verify;
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
-    bool profiling = false;
+    int profiling = 0;
     vx_step_profile last_prof{};
     ~vx_spec() {
         if (h_stage) (void)hipHostFree(h_stage);
@@ -1281,13 +1281,16 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
                            d_last + n, d_last + 2 * n, n, D, (uint32_t)e->seed, (uint32_t)(e->seed >> 32));
         VX_HIP(hipGetLastError());
     }
-    const bool prof = e->profiling;
+    // profiling 1: events around every kernel and at the phase boundaries;
+    // 2: phase boundaries only (the round runs undisturbed)
+    const bool prof = e->profiling != 0;
+    const bool per_kernel = e->profiling == 1;
     if (prof) {
         for (int j = 0; j < 4; j++)
             if (!e->ev[j]) VX_HIP(hipEventCreate(&e->ev[j]));
         e->prof_draft.reset();
         e->prof_verify.reset();
-        e->prof_draft.on = e->prof_verify.on = true;
+        e->prof_draft.on = e->prof_verify.on = per_kernel;
         VX_HIP(hipEventRecord(e->ev[0], st));
     }
     // KV bytes read per verify layer (K and V of every visible position)
@@ -1303,7 +1306,7 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
         // step i's input: the last tokens, then column i - 1 of cand [n, D]
         const uint32_t *in_ids = i == 0 ? d_last : cand + (i - 1);
         VX_TRY(forward_dev(e->draft, e->dp, in_ids, metas[i], dm + boff[i], 0, dl, e->draft->ws.p, e->draft->ws.n,
-                           st, prof ? &e->prof_draft : nullptr, kv_draft, stoch ? nullptr : amax_v, amax_i,
+                           st, per_kernel ? &e->prof_draft : nullptr, kv_draft, stoch ? nullptr : amax_v, amax_i,
                            &fused_amax, i == 0 ? 1 : D));
         if (!stoch && fused_amax) {
             VX_TRY(argmax_accept_partials_launch(amax_v, amax_i, (int)amax_chunks, n, 0, 1, nullptr, 0, nullptr,
@@ -1323,7 +1326,7 @@ extern "C" int vx_spec_step(vx_spec *e, const int64_t *state_ids, int64_t n, int
     if (prof) VX_HIP(hipEventRecord(e->ev[1], st));
     bool verify_amax = false;
     VX_TRY(forward_dev(e->target, e->tp, (const uint32_t *)e->d_vids.p, metas[D], dm + boff[D], 1, e->d_tlog.p,
-                       e->target->ws.p, e->target->ws.n, st, prof ? &e->prof_verify : nullptr, kv_verify,
+                       e->target->ws.p, e->target->ws.n, st, per_kernel ? &e->prof_verify : nullptr, kv_verify,
                        stoch ? nullptr : amax_v, amax_i, &verify_amax));
     if (prof) VX_HIP(hipEventRecord(e->ev[2], st));
     // ---- acceptance (spec.rs:266-292)
@@ -1483,7 +1486,8 @@ extern "C" int vx_spec_last_trace_draft(const vx_spec *e, float *draft_logits, f
 }
 extern "C" int vx_spec_set_profiling(vx_spec *e, int enable) {
     VX_REQUIRE(e, "profiling: null engine");
-    e->profiling = enable != 0;
+    VX_REQUIRE(enable >= 0 && enable <= 2, "profiling: mode is 0, 1 (per kernel) or 2 (phases only)");
+    e->profiling = enable;
     return 0;
 }
 extern "C" int vx_spec_last_profile(const vx_spec *e, vx_step_profile *out) {

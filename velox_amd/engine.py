@@ -263,8 +263,10 @@ class SpecEngine:
                 "streams": streams, "rounds": rounds, "candidates": cand, "verify_logits": logits,
                 "draft_logits": dl, "uniforms": uni}
 
-    def set_profiling(self, enable: bool):
-        check(lib.vx_spec_set_profiling(self._h, 1 if enable else 0))
+    def set_profiling(self, enable, phases_only: bool = False):
+        """Per-kernel HIP-event timing (enable), or only the draft / verify /
+        accept phase boundaries (phases_only: the kernels run undisturbed)."""
+        check(lib.vx_spec_set_profiling(self._h, (2 if phases_only else 1) if enable else 0))
 
     def last_profile(self) -> dict:
         p = StepProfile()
