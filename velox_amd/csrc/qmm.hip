@@ -1222,6 +1222,145 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     }
 }
 
+// Epilogue of the eight-wave kernel with one 32-column tile per wave pair.
+// The MFMA ran with the weights as its A operand, so accumulator element i
+// of lane L is row m0 + 32t + L%32, tile column 8(i/4) + 4(L/32) + i%4: each
+// register quad holds four consecutive columns of one row.  The k-halves
+// split the quads: half kh keeps quads kh and kh + 2 (for SwiGLU the gate
+// and the up columns of the same four features) and takes the partner's sum
+// of them from LDS (own + partner, the same sum either way round).  Each
+// wave then finishes its quads from registers: 16-byte f32 partials, 8-byte
+// f16 / bf16 outputs, no row-major staging.  RDT is the rounding dtype.
+template <int RDT, int MT>
+__device__ __forceinline__ void k2_finish(const QmmArgs &a, const floatx16 (&acc)[MT][1], float4 *xs, int m0,
+                                          int colb, int sp, int kh, int wc, int lane, int tid, bool live) {
+    const int h = lane >> 5;
+    const int tile = colb / 32 + wc;
+    const bool tile_ok = live && tile * 32 < a.N;
+    // hand over the quads the partner keeps: (1 - kh) + 2j
+    float4 *mine = xs + (wc * 2 + kh) * MT * 2 * 64 + lane;
+    const float4 *theirs = xs + (wc * 2 + (kh ^ 1)) * MT * 2 * 64 + lane;
+    __syncthreads();  // every wave is past its last read of the activation ring
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int g0 = 4 * (2 * j), g1 = 4 * (1 + 2 * j);
+            mine[(t * 2 + j) * 64] = kh ? make_float4(acc[t][0][g0], acc[t][0][g0 + 1], acc[t][0][g0 + 2], acc[t][0][g0 + 3])
+                                        : make_float4(acc[t][0][g1], acc[t][0][g1 + 1], acc[t][0][g1 + 2], acc[t][0][g1 + 3]);
+        }
+    __syncthreads();
+    // own quads kh + 2j, summed with the partner's
+    float v[MT][2][4];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int g0 = 4 * (2 * j), g1 = 4 * (1 + 2 * j);
+            const float4 o = theirs[(t * 2 + j) * 64];
+            const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[t][j][q] = (kh ? acc[t][0][g1 + q] : acc[t][0][g0 + q]) + ov[q];
+        }
+    const bool partial = a.splits > 1 || a.epi == kEpiPartial;
+    if (a.epi == VX_EPI_SWIGLU && !partial) {
+        // features 16 tile + 8 kh + 4h + q: gate in quad kh, up in quad kh + 2
+        const int f0 = 16 * tile + 8 * kh + 4 * h;
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int row = m0 + 32 * t + (lane & 31);
+            if (!tile_ok || row >= a.M) continue;
+            float o[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float g = round_to<RDT>(v[t][0][q] * a.acc_scale);
+                const float u = round_to<RDT>(v[t][1][q] * a.acc_scale);
+                o[q] = round_to<RDT>(round_to<RDT>(silu_f(g)) * u) * a.store_scale;
+            }
+            store4_dt(a.y, (int64_t)row * (a.N / 2) + f0, o, a.y_dt);
+        }
+        return;
+    }
+    const bool amax = a.amax_v != nullptr && !partial;
+    float *cand_v = (float *)(xs + 4 * 2 * MT * 2 * 64);
+    uint32_t *cand_i = (uint32_t *)(cand_v + 8 * MT * 32);
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const int row = m0 + 32 * t + (lane & 31);
+        const bool ok = tile_ok && row < a.M;
+        float bv = -__builtin_inff();
+        uint32_t bi = 0xffffffffu;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = tile * 32 + 8 * (kh + 2 * j) + 4 * h;
+            if (partial) {
+                if (ok) *(float4 *)(a.partial + ((int64_t)sp * a.M + row) * a.N + col) =
+                    make_float4(v[t][j][0], v[t][j][1], v[t][j][2], v[t][j][3]);
+                continue;
+            }
+            const int64_t idx = (int64_t)row * a.N + col;
+            float rv[4] = {0.f, 0.f, 0.f, 0.f}, o[4];
+            if (ok && a.epi == VX_EPI_RESIDUAL) load4_dt(a.resid, idx, rv, a.y_dt);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float x = round_to<RDT>(v[t][j][q] * a.acc_scale);
+                if (a.epi == VX_EPI_RESIDUAL) x = round_to<RDT>(rv[q] + x);
+                o[q] = x * a.store_scale;
+            }
+            if (ok) store4_dt(a.y, idx, o, a.y_dt);
+            if (amax) {
+                // columns ascend with j and q: strict > keeps the first index
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float x = round_dt(o[q], a.y_dt);
+                    if (ok && x > bv) {  // NaN never wins
+                        bv = x;
+                        bi = (uint32_t)(col + q);
+                    }
+                }
+            }
+        }
+        if (amax) {
+            // the other half-wave holds the same row's other columns
+            const float ov = __shfl_xor(bv, 32);
+            const uint32_t oi = (uint32_t)__shfl_xor((int)bi, 32);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+            if (h == 0) {
+                cand_v[((wc * 2 + kh) * MT + t) * 32 + lane] = bv;
+                cand_i[((wc * 2 + kh) * MT + t) * 32 + lane] = bi;
+            }
+        }
+    }
+    if (amax) {
+        // one (value, first index) per row and workgroup (128 columns) at
+        // [row * ceil(N/128) + column block]: the best of the eight waves'
+        // candidates (the order-free rule: larger value, then smaller index)
+        __syncthreads();
+        if (tid < MT * 32 && live) {
+            const int row = m0 + tid;
+            if (row < a.M) {
+                float bv = -__builtin_inff();
+                uint32_t bi = 0xffffffffu;
+#pragma unroll
+                for (int w = 0; w < 8; w++) {
+                    const float ov = cand_v[(w * MT + tid / 32) * 32 + tid % 32];
+                    const uint32_t oi = cand_i[(w * MT + tid / 32) * 32 + tid % 32];
+                    if (ov > bv || (ov == bv && oi < bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                const int64_t at = (int64_t)row * ((a.N + 127) / 128) + colb / 128;
+                a.amax_v[at] = bv;
+                a.amax_i[at] = bi;
+            }
+        }
+    }
+}
+
 // The packed GEMM on eight waves: waves w and w+4 share the 32-column tiles
 // of slot w%4 and split each 128-wide k step, the first taking MFMAs 0..3
 // (packed words 0..3, the step's first scale group), the second MFMAs 4..7.
@@ -1229,10 +1368,9 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
 // costs half the MFMA chain of the four-wave kernel, and each wave streams
 // half the weight bytes.  Activations arrive by LDS DMA as in
 // qmm_f16_dma_kernel (MT DMA instructions per wave per step); the two
-// halves' accumulators are summed through LDS once, at the end, by the
-// first wave of each pair.  No early exit: surplus workgroups of the last
-// XCD row recompute the last item and store nothing, so every kernel
-// argument is requested in one batch at entry.
+// halves' accumulators meet in LDS once, at the end.  No early exit:
+// surplus workgroups of the last XCD row recompute the last item and store
+// nothing, so every kernel argument is requested in one batch at entry.
 template <int MT, int NT, int P>
 __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     constexpr int R = P + 1;
@@ -1244,7 +1382,7 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     static_assert(VM < 64, "vmcnt range");
     constexpr int XSLOTS = R * BUF;
     constexpr int CSLOTS = 4 * MT * NT * 16 * 64 / 4;  // float4 slots of the pair combine
-    constexpr int RSLOTS = 4 * MT * 32 * kRowStride / 4 + 4 * MT * 32 * 8 / 16;  // ... row-major tiles + argmax
+    constexpr int RSLOTS = 8 * MT * 2 * 64 + 8 * MT * 32 * 2 / 4;  // ... of k2_finish: quads + argmax candidates
     constexpr int ESLOTS = CSLOTS > RSLOTS ? CSLOTS : RSLOTS;
     __shared__ __align__(256) uint4 xs[XSLOTS > ESLOTS ? XSLOTS : ESLOTS];
 
@@ -1360,8 +1498,14 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-                for (int t = 0; t < MT; t++)
-                    acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[jj & 1][t], bq[jj & 1][nt], acc[t][nt], 0, 0, 0);
+                for (int t = 0; t < MT; t++) {
+                    // one column tile per wave: weights as the A operand, so
+                    // each register quad holds four columns of one row
+                    if constexpr (NT == 1)
+                        acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bq[jj & 1][nt], af[jj & 1][t], acc[t][nt], 0, 0, 0);
+                    else
+                        acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[jj & 1][t], bq[jj & 1][nt], acc[t][nt], 0, 0, 0);
+                }
         }
     };
 
@@ -1385,15 +1529,13 @@ __global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
     vm_wait<0>();
 
     if constexpr (NT == 1) {
-        // the pair's sum is formed in LDS as row-major tiles, then all eight
-        // waves finish four columns at a time
-        float *tile0 = (float *)xs + wc * MT * 32 * kRowStride;
-        __syncthreads();
-        if (kh == 1) acc_to_rows<MT>(acc, tile0, lane, false);
-        __syncthreads();
-        if (kh == 0) acc_to_rows<MT>(acc, tile0, lane, true);
-        __syncthreads();
-        finish_rows<MT, 512>(a, (const float *)xs, m0, cb * (kWaves * 32), sp, tid, live);
+        float4 *ex = (float4 *)xs;
+        if (a.round_dt == VX_BF16)
+            k2_finish<VX_BF16, MT>(a, acc, ex, m0, cb * (kWaves * 32), sp, kh, wc, lane, tid, live);
+        else if (a.round_dt == VX_F16)
+            k2_finish<VX_F16, MT>(a, acc, ex, m0, cb * (kWaves * 32), sp, kh, wc, lane, tid, live);
+        else
+            k2_finish<VX_F32, MT>(a, acc, ex, m0, cb * (kWaves * 32), sp, kh, wc, lane, tid, live);
         return;
     }
 

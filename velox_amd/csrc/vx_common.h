@@ -53,9 +53,11 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
 }
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     // round to nearest even; NaN kept quiet
-    uint32_t x = __float_as_uint(f);
-    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-    return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+    // (a select, not a branch: a per-element branch diverges the wave)
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t rne = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+    const uint32_t qnan = (x >> 16) | 0x40u;
+    return (uint16_t)((x & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(vx_half, h);
