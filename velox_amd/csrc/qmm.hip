@@ -1222,6 +1222,31 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     }
 }
 
+// Rounding and stores of the eight-wave epilogue on gfx950's converts:
+// v_cvt_pk_bf16_f32 and v_cvt_f16_f32 round to nearest even like the
+// software rounding (a NaN stays a NaN, its payload is not kept).
+template <int DT>
+__device__ __forceinline__ float round_hw(float v) {
+    if constexpr (DT == VX_BF16) return (float)(__bf16)v;
+    else if constexpr (DT == VX_F16) return (float)(vx_half)v;
+    else return v;
+}
+__device__ __forceinline__ void store4_hw(void *y, int64_t i, const float (&v)[4], int dt) {
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    typedef vx_half halfx4_t __attribute__((ext_vector_type(4)));
+    if (dt == VX_F32) {
+        *(float4 *)((float *)y + i) = make_float4(v[0], v[1], v[2], v[3]);
+    } else if (dt == VX_BF16) {
+        const bf16x4_t h = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+        *(uint2 *)((uint16_t *)y + i) = __builtin_bit_cast(uint2, h);
+    } else {
+        const halfx4_t h = {(vx_half)v[0], (vx_half)v[1], (vx_half)v[2], (vx_half)v[3]};
+        *(uint2 *)((uint16_t *)y + i) = __builtin_bit_cast(uint2, h);
+    }
+}
+// SiLU with the hardware reciprocal (1 ulp) in place of an IEEE division
+__device__ __forceinline__ float silu_hw(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
 // Epilogue of the eight-wave kernel with one 32-column tile per wave pair.
 // The MFMA ran with the weights as its A operand, so accumulator element i
 // of lane L is row m0 + 32t + L%32, tile column 8(i/4) + 4(L/32) + i%4: each
@@ -1273,11 +1298,11 @@ __device__ __forceinline__ void k2_finish(const QmmArgs &a, const floatx16 (&acc
             float o[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const float g = round_to<RDT>(v[t][0][q] * a.acc_scale);
-                const float u = round_to<RDT>(v[t][1][q] * a.acc_scale);
-                o[q] = round_to<RDT>(round_to<RDT>(silu_f(g)) * u) * a.store_scale;
+                const float g = round_hw<RDT>(v[t][0][q] * a.acc_scale);
+                const float u = round_hw<RDT>(v[t][1][q] * a.acc_scale);
+                o[q] = round_hw<RDT>(round_hw<RDT>(silu_hw(g)) * u) * a.store_scale;
             }
-            store4_dt(a.y, (int64_t)row * (a.N / 2) + f0, o, a.y_dt);
+            store4_hw(a.y, (int64_t)row * (a.N / 2) + f0, o, a.y_dt);
         }
         return;
     }
@@ -1303,11 +1328,11 @@ __device__ __forceinline__ void k2_finish(const QmmArgs &a, const floatx16 (&acc
             if (ok && a.epi == VX_EPI_RESIDUAL) load4_dt(a.resid, idx, rv, a.y_dt);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                float x = round_to<RDT>(v[t][j][q] * a.acc_scale);
-                if (a.epi == VX_EPI_RESIDUAL) x = round_to<RDT>(rv[q] + x);
+                float x = round_hw<RDT>(v[t][j][q] * a.acc_scale);
+                if (a.epi == VX_EPI_RESIDUAL) x = round_hw<RDT>(rv[q] + x);
                 o[q] = x * a.store_scale;
             }
-            if (ok) store4_dt(a.y, idx, o, a.y_dt);
+            if (ok) store4_hw(a.y, idx, o, a.y_dt);
             if (amax) {
                 // columns ascend with j and q: strict > keeps the first index
 #pragma unroll
