@@ -1397,7 +1397,7 @@ __device__ __forceinline__ void k2_finish(const QmmArgs &a, const floatx16 (&acc
 // surplus workgroups of the last XCD row recompute the last item and store
 // nothing, so every kernel argument is requested in one batch at entry.
 template <int MT, int NT, int P>
-__global__ __launch_bounds__(512) void qmm_f16_k2_kernel(QmmArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void qmm_f16_k2_kernel(QmmArgs a) {
     constexpr int R = P + 1;
     static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
     constexpr int UX = MT;
