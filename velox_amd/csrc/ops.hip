@@ -345,29 +345,34 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(AcceptArgs a) {
 // The partials never hold NaN (it never wins a chunk), so arg_better is a
 // total order on them and the 64 lanes may combine a row's chunks strided and
 // then by butterfly: the same winner as the sequential scan.
-__global__ __launch_bounds__(64) void accept_finish_kernel(AcceptArgs a) {
+// One wave per row of the group (up to kAcceptWaves, then strided): the
+// row's partials are requested 24 per lane at a time (one memory round trip
+// for up to 1536 partials, the LM head's 1187), and rows run in parallel.
+constexpr int kAcceptWaves = 8;
+__global__ __launch_bounds__(64 * kAcceptWaves) void accept_finish_kernel(AcceptArgs a) {
     __shared__ uint32_t am[64];
     const int64_t grp = blockIdx.x;
-    for (int rr = 0; rr < a.rows_per_group; rr++) {
+    const int lane = threadIdx.x & 63;
+    const int waves = blockDim.x >> 6;
+    for (int rr = threadIdx.x >> 6; rr < a.rows_per_group; rr += waves) {
         const int64_t rw = grp * a.rows_per_group + rr;
         ArgBest best = {-__builtin_inff(), 0xffffffffu};
-        // eight partials per lane in flight per batch
-        for (int c0 = threadIdx.x; c0 < a.n_chunks; c0 += 64 * 8) {
-            float v[8];
-            uint32_t ix[8];
+        for (int c0 = lane; c0 < a.n_chunks; c0 += 64 * 24) {
+            float v[24];
+            uint32_t ix[24];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < 24; u++) {
                 const int c = c0 + 64 * u;
                 v[u] = c < a.n_chunks ? a.pv[rw * a.n_chunks + c] : -__builtin_inff();
                 ix[u] = c < a.n_chunks ? a.pi[rw * a.n_chunks + c] : 0xffffffffu;
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) best = arg_better(best, {v[u], ix[u]});
+            for (int u = 0; u < 24; u++) best = arg_better(best, {v[u], ix[u]});
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1)
             best = arg_better(best, {__shfl_xor(best.v, o), (uint32_t)__shfl_xor((int)best.i, o)});
-        if (threadIdx.x == 0) {
+        if (lane == 0) {
             const uint32_t idx = best.i == 0xffffffffu ? 0u : best.i;
             am[rr] = idx;
             if (a.argmax_out) a.argmax_out[rw] = idx;
@@ -768,7 +773,8 @@ int argmax_accept_launch(const void *logits, int ldt, int64_t rows, int64_t voca
         hipLaunchKernelGGL(argmax_partial_kernel<VX_F16>, grid, dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL(argmax_partial_kernel<VX_F32>, grid, dim3(256), 0, st, a);
-    hipLaunchKernelGGL(accept_finish_kernel, dim3((unsigned)(rows / rows_per_group)), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(accept_finish_kernel, dim3((unsigned)(rows / rows_per_group)),
+                       dim3(64 * std::min(rows_per_group, kAcceptWaves)), 0, st, a);
     VX_HIP(hipGetLastError());
     return 0;
 }
@@ -795,7 +801,8 @@ int argmax_accept_partials_launch(const float *pv, const uint32_t *pi, int n_chu
     a.tokens = tokens;
     a.next_ids = next_ids;
     a.next_stride = next_stride;
-    hipLaunchKernelGGL(accept_finish_kernel, dim3((unsigned)(rows / rows_per_group)), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(accept_finish_kernel, dim3((unsigned)(rows / rows_per_group)),
+                       dim3(64 * std::min(rows_per_group, kAcceptWaves)), 0, st, a);
     VX_HIP(hipGetLastError());
     return 0;
 }
