@@ -227,9 +227,10 @@ def run_spec(args):
         log("[bench] profile " + json.dumps({kk: round(v, 4) for kk, v in agg.items()}))
         qmm_gbs = agg["verify_qmm_bytes"] / (agg["verify_qmm_ms"] * 1e-3) / 1e9
         verify_bytes = agg["verify_qmm_bytes"] + agg["verify_attention_bytes"]
-        verify_gbs = verify_bytes / (agg["verify_ms"] * 1e-3) / 1e9
     else:  # no profiled rounds (e.g. under a profiler): no live kernel figures
-        agg, qmm_gbs, verify_bytes, verify_gbs = None, None, None, None
+        agg, qmm_gbs, verify_bytes = None, None, None
+    phase_ms = None if not phases else {
+        kk: float(np.mean([p[kk] for p in phases])) for kk in ("draft_ms", "verify_ms", "accept_ms")}
     # the measured device copy rate, reported next to the published peak
     copy_gbs = device_copy_gbs() if profs else None
     # the same GEMM ops against the dense f16 MFMA peak: algorithmic flops
@@ -255,9 +256,12 @@ def run_spec(args):
                    "global_batch": B, "k": k, "prompt_len": args.prompt, "context_at_end": ctx,
                    "seq_len": ctx, "parallelism": "single GPU"},
         "acceptance_rate": accepted / (args.steps * B * k),
-        "verify_step": None if agg is None else {
-            "ms": agg["verify_ms"], "algorithmic_bytes": verify_bytes, "hbm_gbs": verify_gbs,
-            "draft_ms": agg["draft_ms"], "accept_ms": agg["accept_ms"]},
+        # the verify phase of undisturbed rounds (events at its boundaries
+        # only) over the algorithmic bytes of its GEMMs and attention
+        "verify_step": None if (agg is None or not phases) else {
+            "ms": phase_ms["verify_ms"], "algorithmic_bytes": verify_bytes,
+            "hbm_gbs": verify_bytes / (phase_ms["verify_ms"] * 1e-3) / 1e9,
+            "draft_ms": phase_ms["draft_ms"], "accept_ms": phase_ms["accept_ms"]},
         "roofline": {"bound": "hbm",
                      "kernel": "qmm_f16_k2_kernel: the verify step's int4 GEMMs (36 layers "
                                "x qkv, o, gate|up with its SwiGLU finish, down; plus the LM head), average per op",
@@ -276,8 +280,7 @@ def run_spec(args):
         "decisions_check": "ok" if decisions_ok else "mismatch",
         # phase times of undisturbed rounds (they sum to about ms_per_step;
         # the commit's host work is the remainder)
-        "kernel_breakdown_ms": None if not phases else {
-            kk: float(np.mean([p[kk] for p in phases])) for kk in ("draft_ms", "verify_ms", "accept_ms")},
+        "kernel_breakdown_ms": phase_ms,
         # per-class sums from the per-kernel event rounds: each event pair also
         # brackets its kernel's dispatch gap, so these run above the phases
         "kernel_class_ms_event_bracketed": None if agg is None else {

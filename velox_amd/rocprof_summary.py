@@ -13,6 +13,9 @@
     python -m velox_amd.rocprof_summary calib RESULTS.db --bytes B
         FETCH_SIZE or WRITE_SIZE (KiB) read for the largest
         __amd_rocclr_copyBuffer dispatch, and the byte factor B / (KiB * 1024)
+    python -m velox_amd.rocprof_summary pmc RESULTS.db|counter_collection.csv --kernel REGEX [--skip N]
+        mean per dispatch of every counter over the dispatches whose kernel
+        name matches REGEX (the first N of them skipped as warm-up)
 
 The kernel-trace duration of a dispatch is end - start (ns).
 """
@@ -47,7 +50,15 @@ def dispatches(db: str):
 
 
 def counters(db: str):
-    """{dispatch_id: {counter: value}} from a --pmc run."""
+    """{dispatch_id: {counter: value}} from a --pmc run (results database or
+    the counter_collection.csv of `--output-format csv`)."""
+    if db.endswith(".csv"):
+        import csv
+
+        out = collections.defaultdict(dict)
+        for r in csv.DictReader(open(db)):
+            out[int(r["Dispatch_Id"])][r["Counter_Name"]] = float(r["Counter_Value"])
+        return out
     c = sqlite3.connect(db)
     cols = [r[1] for r in c.execute("pragma table_info('counters_collection')")]
     out = collections.defaultdict(dict)
@@ -126,6 +137,30 @@ def cmd_calib(args):
           f"factor = {args.bytes / (v * 1024):.4f}")
 
 
+def cmd_pmc(args):
+    """Mean counter values per dispatch of one kernel."""
+    pm = counters(args.db)
+    if args.db.endswith(".csv"):
+        import csv
+
+        names = {}
+        for r in csv.DictReader(open(args.db)):
+            names[int(r["Dispatch_Id"])] = _short(r["Kernel_Name"])
+    else:
+        names = {d: n for n, _, _, _, _, d in dispatches(args.db)}
+    sel = sorted(d for d, n in names.items() if re.search(args.kernel, n))[args.skip:]
+    if not sel:
+        print("no matching dispatches")
+        return
+    tot = collections.Counter()
+    for d in sel:
+        for k, v in pm.get(d, {}).items():
+            tot[k] += v
+    print(f"{len(sel)} dispatches of {names[sel[0]]} (first {args.skip} matching skipped)")
+    for k in sorted(tot):
+        print(f"  {k:28s} {tot[k] / len(sel):16.1f}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -137,11 +172,15 @@ def main():
     b.add_argument("--rounds", type=int, default=4)
     b.add_argument("--total-rounds", type=int, default=6)
     b.add_argument("--pmc", nargs="*")
+    d = sub.add_parser("pmc")
+    d.add_argument("db")
+    d.add_argument("--kernel", required=True)
+    d.add_argument("--skip", type=int, default=0)
     c = sub.add_parser("calib")
     c.add_argument("db")
     c.add_argument("--bytes", type=float, required=True)
     args = ap.parse_args()
-    {"trace": cmd_trace, "verify": cmd_verify, "calib": cmd_calib}[args.cmd](args)
+    {"trace": cmd_trace, "verify": cmd_verify, "calib": cmd_calib, "pmc": cmd_pmc}[args.cmd](args)
 
 
 if __name__ == "__main__":
