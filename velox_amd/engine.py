@@ -14,6 +14,16 @@ from ._lib import (F16, LayerHost, QLinearHost, QwenConfig, RoundOutcome, RoundT
                    VeloxError, WeightsHost, check, lib)
 
 
+def close_dependents(owner) -> None:
+    """Close the native objects whose destruction reaches into `owner` (a
+    scheduler frees its states' pages through the engine) before `owner`
+    itself goes.  Python finalises objects of one garbage cycle in no set
+    order (PEP 442), and at interpreter exit whatever is left goes that way,
+    so the owner closes them first; a closed dependent is a no-op."""
+    for d in list(getattr(owner, "_dependents", ())):
+        d.close()
+
+
 class PagedKvCache:
     """pages.rs:82-255: per-layer K/V pools [P, h_kv, page_size, d] (f16 on the
     device), LIFO free list (page 0 first), refcounts, all-or-nothing alloc."""
@@ -55,8 +65,8 @@ class PagedKvCache:
     def layer_pool_ptr(self, layer, kv):
         return lib.vx_pages_pool(self._h, layer, kv)
 
-    def __del__(self, _destroy=lib.vx_pages_destroy):  # bound now: module globals may be gone at exit
-        close_dependents(self)
+    def __del__(self, _destroy=lib.vx_pages_destroy, _close=close_dependents):  # bound now: globals may be gone at exit
+        _close(self)
         if getattr(self, "_h", None):
             _destroy(self._h)
             self._h = None
@@ -146,16 +156,6 @@ class PagedQwen3:
         if getattr(self, "_h", None):
             _destroy(self._h)
             self._h = None
-
-
-def close_dependents(owner) -> None:
-    """Close the native objects whose destruction reaches into `owner` (a
-    scheduler frees its states' pages through the engine) before `owner`
-    itself goes.  Python finalises objects of one garbage cycle in no set
-    order (PEP 442), and at interpreter exit whatever is left goes that way,
-    so the owner closes them first; a closed dependent is a no-op."""
-    for d in list(getattr(owner, "_dependents", ())):
-        d.close()
 
 
 @dataclass
@@ -283,8 +283,8 @@ class SpecEngine:
     def free(self, state):
         lib.vx_spec_free(self._h, state.id)
 
-    def __del__(self, _destroy=lib.vx_spec_destroy):  # bound now: module globals may be gone at exit
-        close_dependents(self)
+    def __del__(self, _destroy=lib.vx_spec_destroy, _close=close_dependents):  # bound now: globals may be gone at exit
+        _close(self)
         if getattr(self, "_h", None):
             _destroy(self._h)
             self._h = None
