@@ -119,7 +119,6 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     constexpr int DK = D / 32;  // MFMA k-steps over head_dim
     constexpr int DT = D / 16;  // output row tiles of O^T
     constexpr int VT_STRIDE = kKeyBlock + 4;  // halves per transposed V row (bank spread)
-    constexpr int CSLOTS = DT * QT * 4 + 2 * QT;  // floats per lane in the wave merge
     // per-wave V^T tiles during the key loop; the merge buffers afterwards
     __shared__ __attribute__((aligned(16))) unsigned char smem[attn_lds_bytes<KT, D, QT>()];
 
@@ -439,19 +438,16 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     // summing the waves in wave order (deterministic)
     constexpr int TPW = DT >= kAttnWaves ? DT / kAttnWaves : 1;
     __syncthreads();  // every wave is done with its V^T tile
-    float *comb = (float *)smem;
-    {
-        float *dst = comb + (size_t)wave * CSLOTS * 64 + lane;
-        int slot = 0;
+    // 16-byte slots: O tile i of query tile qt of wave w at
+    // ((w * QT + qt) * DT + i) * 64 + lane, then (m, l) pairs at
+    // (w * QT + qt) * 64 + lane (the same LDS as the four-byte layout)
+    floatx4 *comb4 = (floatx4 *)smem;
+    float2 *combml = (float2 *)(comb4 + (size_t)kAttnWaves * QT * DT * 64);
 #pragma unroll
-        for (int qt = 0; qt < QT; qt++) {
-            dst[(slot++) * 64] = m_run[qt];
-            dst[(slot++) * 64] = l_run[qt];
+    for (int qt = 0; qt < QT; qt++) {
+        combml[(wave * QT + qt) * 64 + lane] = make_float2(m_run[qt], l_run[qt]);
 #pragma unroll
-            for (int i = 0; i < DT; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) dst[(slot++) * 64] = o[i][qt][r];
-        }
+        for (int i = 0; i < DT; i++) comb4[((wave * QT + qt) * DT + i) * 64 + lane] = o[i][qt];
     }
     __syncthreads();
     const int i_lo = wave * TPW;
@@ -460,13 +456,13 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     float mm[QT], lm[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; qt++) {
-        const int base = qt * (2 + DT * 4);
-        float mw[kAttnWaves], fw[kAttnWaves];
+        float2 mlw[kAttnWaves];
+        float fw[kAttnWaves];
         float M = -__builtin_inff();
 #pragma unroll
         for (int w = 0; w < kAttnWaves; w++) {
-            mw[w] = comb[((size_t)w * CSLOTS + base) * 64 + lane];
-            M = fmaxf(M, mw[w]);
+            mlw[w] = combml[(w * QT + qt) * 64 + lane];
+            M = fmaxf(M, mlw[w].x);
         }
         const bool dead = M == -__builtin_inff();
         float L = 0.f;
@@ -474,13 +470,14 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
         for (int t = 0; t < TPW; t++) om[t][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < kAttnWaves; w++) {
-            fw[w] = dead ? 0.f : exp2f(mw[w] - M);
-            L += comb[((size_t)w * CSLOTS + base + 1) * 64 + lane] * fw[w];
+            fw[w] = dead ? 0.f : exp2f(mlw[w].x - M);
+            L += mlw[w].y * fw[w];
 #pragma unroll
-            for (int t = 0; t < TPW; t++)
+            for (int t = 0; t < TPW; t++) {
+                const floatx4 ow = comb4[((w * QT + qt) * DT + i_lo + t) * 64 + lane];
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    om[t][qt][r] += comb[((size_t)w * CSLOTS + base + 2 + (i_lo + t) * 4 + r) * 64 + lane] * fw[w];
+                for (int r = 0; r < 4; r++) om[t][qt][r] += ow[r] * fw[w];
+            }
         }
         mm[qt] = M;
         lm[qt] = L;
