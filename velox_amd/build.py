@@ -3,7 +3,8 @@
 Every translation unit is compiled in parallel (the .hip files by hipcc,
 the host-only .cpp files by g++), then linked into velox_amd/libvelox_hip.so.
 Packed-FP32 instruction selection is disabled (`-packed-fp32-ops`) for all
-device code.
+device code, and kernel-argument preloading is on (the leading scalar
+arguments of a kernel arrive in SGPRs).
 """
 from __future__ import annotations
 
@@ -26,6 +27,9 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(ROOT, "include"), "-Wall", "-Wno-unused-function",
     "-Wno-unused-variable", "-Wno-unused-result",
+    # gfx950 kernarg preload: a kernel's leading scalar arguments arrive in
+    # SGPRs at wave launch instead of by a load from the argument block
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

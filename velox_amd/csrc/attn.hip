@@ -113,8 +113,24 @@ constexpr size_t attn_lds_bytes() {
 // FUSE: the instantiation that finishes q/k/v from the qkv partials (a.qkv);
 // the plain one compiles without that prologue, whose register arrays would
 // otherwise set the register allocation (and occupancy) of every launch.
+// The arguments read before the first memory round trip (work item, block
+// table, row metadata) also come first as scalars, which the compiler
+// preloads into SGPRs at wave launch; they overwrite their copies in `a`.
 template <int KT, int D, int QT, bool FUSE>
-__global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void paged_attn_kernel(const uint32_t *bt_arg, const uint32_t *cu_arg,
+                                                         const uint32_t *kvo_arg, int n_splits_arg, int n_qtiles_arg,
+                                                         int h_kv_arg, int max_blocks_arg, int chunk_arg, int ps_arg,
+                                                         int mode_arg, AttnArgs a) {
+    a.bt = bt_arg;
+    a.cu = cu_arg;
+    a.kvo = kvo_arg;
+    a.n_splits = n_splits_arg;
+    a.n_qtiles = n_qtiles_arg;
+    a.h_kv = h_kv_arg;
+    a.max_blocks = max_blocks_arg;
+    a.chunk = chunk_arg;
+    a.ps = ps_arg;
+    a.mode = mode_arg;
     typedef typename MfmaT<KT>::frag frag;
     constexpr int DK = D / 32;  // MFMA k-steps over head_dim
     constexpr int DT = D / 16;  // output row tiles of O^T
@@ -629,10 +645,12 @@ template <int KT, int D, int QT>
 void launch_attn(const AttnArgs &a, int64_t n_items, hipStream_t st) {
     if (a.qkv)
         hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT, true>), dim3((unsigned)n_items), dim3(64 * kAttnWaves), 0,
-                           st, a);
+                           st, a.bt, a.cu, a.kvo, a.n_splits, a.n_qtiles, a.h_kv, a.max_blocks, a.chunk, a.ps, a.mode,
+                           a);
     else
         hipLaunchKernelGGL((paged_attn_kernel<KT, D, QT, false>), dim3((unsigned)n_items), dim3(64 * kAttnWaves), 0,
-                           st, a);
+                           st, a.bt, a.cu, a.kvo, a.n_splits, a.n_qtiles, a.h_kv, a.max_blocks, a.chunk, a.ps, a.mode,
+                           a);
 }
 
 template <int KT>

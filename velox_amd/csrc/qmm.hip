@@ -1066,7 +1066,12 @@ __device__ __forceinline__ void vm_wait() {
 // every wave's DMA visible and proves that the buffer refilled next was
 // read to the end by everyone.
 template <int MT, int NT, int P>
-__global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
+// leading scalars: the prologue's arguments, preloaded into SGPRs (see
+// qmm_f16_k2_kernel)
+__global__ __launch_bounds__(256) void qmm_f16_dma_kernel(const uint16_t *x_arg, const uint8_t *w_arg, int M_arg,
+                                                          int N_arg, int K_arg, int S_arg, int sps_arg,
+                                                          int splits_arg, int per_xcd_arg, int total_items_arg,
+                                                          QmmArgs a) {
     constexpr int R = P + 1;
     static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
     constexpr int UX = 2 * MT;             // DMA instructions per wave per step
@@ -1077,13 +1082,13 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     __shared__ __align__(256) uint4 xs[R * BUF];
 
     const int bid = blockIdx.x;
-    const int item = (bid & 7) * a.per_xcd + (bid >> 3);
-    if (item >= a.total_items) return;
-    const int cb = item / a.splits;
-    const int sp = item - cb * a.splits;
+    const int item = (bid & 7) * per_xcd_arg + (bid >> 3);
+    if (item >= total_items_arg) return;
+    const int cb = item / splits_arg;
+    const int sp = item - cb * splits_arg;
     const int m0 = blockIdx.y * MT * 32;
-    const int s_lo = sp * a.sps;
-    const int s_hi = min(a.S, s_lo + a.sps);
+    const int s_lo = sp * sps_arg;
+    const int s_hi = min(S_arg, s_lo + sps_arg);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1092,13 +1097,13 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     // DMA instruction g of wave w fills slots [64 (4g + w), +64): lane l takes
     // row 16g + 4w + l/16 and chunk (l%16) ^ (row%16).  Rows past M re-read
     // row M-1 (finite values whose results are never stored).
-    const uint16_t *xh = (const uint16_t *)a.x;
+    const uint16_t *xh = x_arg;
     int xoff[UX];
     {
         const int rl = 4 * wave + (lane >> 4);
         const int c = (lane & 15) ^ (rl & 15);
 #pragma unroll
-        for (int g = 0; g < UX; g++) xoff[g] = min(m0 + 16 * g + rl, a.M - 1) * a.K + 8 * c;
+        for (int g = 0; g < UX; g++) xoff[g] = min(m0 + 16 * g + rl, M_arg - 1) * K_arg + 8 * c;
     }
     // fragment (j, t) of lane L: row 32t + L%32, chunk 2j + L/32, at byte
     // 8192 t + 256 (L%32) + 16 ((2j + L/32) ^ L%16) = 8192 t + (xrd ^ 32j)
@@ -1109,8 +1114,8 @@ __global__ __launch_bounds__(256) void qmm_f16_dma_kernel(QmmArgs a) {
     const uint8_t *wblk[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const int tile = min(col0 / 32 + nt, a.N / 32 - 1);
-        wblk[nt] = (const uint8_t *)a.w + (int64_t)tile * a.S * kPackBlock;
+        const int tile = min(col0 / 32 + nt, N_arg / 32 - 1);
+        wblk[nt] = w_arg + (int64_t)tile * S_arg * kPackBlock;
     }
     constexpr uint32_t kLoHalf = 0x01000100u, kHiHalf = 0x03020302u;
     const DqConst dq = dq_const();
@@ -1397,7 +1402,13 @@ __device__ __forceinline__ void k2_finish(const QmmArgs &a, const floatx16 (&acc
 // surplus workgroups of the last XCD row recompute the last item and store
 // nothing, so every kernel argument is requested in one batch at entry.
 template <int MT, int NT, int P>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void qmm_f16_k2_kernel(QmmArgs a) {
+// The arguments the prologue needs before its first DMA come first, as
+// scalars: the compiler marks them for preloading into SGPRs at wave launch
+// (gfx950 kernarg preload), so the first requests do not wait on a load of
+// the argument block; the epilogue's fields arrive in `a` meanwhile.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void qmm_f16_k2_kernel(
+    const uint16_t *x_arg, const uint8_t *w_arg, int M_arg, int N_arg, int K_arg, int S_arg, int sps_arg,
+    int splits_arg, int per_xcd_arg, int total_items_arg, QmmArgs a) {
     constexpr int R = P + 1;
     static_assert(R >= 2 && R <= 6, "ring of 2..6 slots");
     constexpr int UX = MT;
@@ -1412,14 +1423,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void q
     __shared__ __align__(256) uint4 xs[XSLOTS > ESLOTS ? XSLOTS : ESLOTS];
 
     const int bid = blockIdx.x;
-    const int item0 = (bid & 7) * a.per_xcd + (bid >> 3);
-    const bool live = item0 < a.total_items;
-    const int item = live ? item0 : a.total_items - 1;
-    const int cb = item / a.splits;
-    const int sp = item - cb * a.splits;
+    const int item0 = (bid & 7) * per_xcd_arg + (bid >> 3);
+    const bool live = item0 < total_items_arg;
+    const int item = live ? item0 : total_items_arg - 1;
+    const int cb = item / splits_arg;
+    const int sp = item - cb * splits_arg;
     const int m0 = blockIdx.y * MT * 32;
-    const int s_lo = sp * a.sps;
-    const int s_hi = min(a.S, s_lo + a.sps);
+    const int s_lo = sp * sps_arg;
+    const int s_hi = min(S_arg, s_lo + sps_arg);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1429,18 +1440,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void q
 
     // DMA instruction g of wave w fills slots [64 (8g + w), +64): lane l takes
     // row 32g + 4w + l/16, chunk (l%16) ^ (row%16).  Rows past M re-read row M-1.
-    const uint16_t *xh = (const uint16_t *)a.x;
+    const uint16_t *xh = x_arg;
     int xoff[UX];
     {
         const int rl = 4 * wave + (lane >> 4);
         const int c = (lane & 15) ^ (rl & 15);
 #pragma unroll
-        for (int g = 0; g < UX; g++) xoff[g] = min(m0 + 32 * g + rl, a.M - 1) * a.K + 8 * c;
+        for (int g = 0; g < UX; g++) xoff[g] = min(m0 + 32 * g + rl, M_arg - 1) * K_arg + 8 * c;
     }
     // DMA instructions whose four rows all lie past M are skipped (those LDS
     // rows only feed accumulator rows that are never stored); the count of
     // live ones is wave-uniform and selects the step's vmcnt immediate
-    const int nx = min(UX, max(0, (a.M - m0 - 4 * wave + 31) / 32));
+    const int nx = min(UX, max(0, (M_arg - m0 - 4 * wave + 31) / 32));
     const uint32_t xs_addr = (uint32_t)(uintptr_t)(lds_void_t *)xs;
     const uint32_t xs_wave = __builtin_amdgcn_readfirstlane(xs_addr + wave * 64 * 16);
     // fragment (j, t), j = 4 kh + jj: byte 8192 t + (xrd ^ 32 j)
@@ -1449,8 +1460,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void q
     const uint8_t *wblk[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const int tile = min(col0 / 32 + nt, a.N / 32 - 1);
-        wblk[nt] = (const uint8_t *)a.w + (int64_t)tile * a.S * kPackBlock;
+        const int tile = min(col0 / 32 + nt, N_arg / 32 - 1);
+        wblk[nt] = w_arg + (int64_t)tile * S_arg * kPackBlock;
     }
     const int wq_off = kh * 1024 + lane * 16;
     const int sb_off = 2048 + (lane & 31) * 8 + kh * 4;
@@ -1815,14 +1826,16 @@ void launch_p32(const QmmArgs &a, const Plan &p, hipStream_t st) {
 template <int MT, int NT, int P>
 void launch_dma(const QmmArgs &a, const Plan &p, hipStream_t st) {
     dim3 grid(p.per_xcd * 8, p.m_blocks);
-    hipLaunchKernelGGL((qmm_f16_dma_kernel<MT, NT, P>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((qmm_f16_dma_kernel<MT, NT, P>), grid, dim3(256), 0, st, (const uint16_t *)a.x,
+                       (const uint8_t *)a.w, a.M, a.N, a.K, a.S, a.sps, a.splits, a.per_xcd, a.total_items, a);
     launch_reduce(a, p, st);
 }
 
 template <int MT, int NT, int P>
 void launch_k2(const QmmArgs &a, const Plan &p, hipStream_t st) {
     dim3 grid(p.per_xcd * 8, p.m_blocks);
-    hipLaunchKernelGGL((qmm_f16_k2_kernel<MT, NT, P>), grid, dim3(512), 0, st, a);
+    hipLaunchKernelGGL((qmm_f16_k2_kernel<MT, NT, P>), grid, dim3(512), 0, st, (const uint16_t *)a.x,
+                       (const uint8_t *)a.w, a.M, a.N, a.K, a.S, a.sps, a.splits, a.per_xcd, a.total_items, a);
     launch_reduce(a, p, st);
 }
 
