@@ -534,6 +534,82 @@ def test_chain_tree_equals_causal(cuda):
     assert np.array_equal(a, b)
 
 
+# Sequences of 33..128 query vectors (rows x query heads per KV head) take the
+# shared-KV kernel: one workgroup per (sequence, KV head, split) stages each
+# key block once for all of them.
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("splits", ["1", "3"])
+def test_shared_kv_attention_head_dims(cuda, monkeypatch, d, dt, splits):
+    """Causal rows, ragged per sequence (17, 9 and 12 rows x 4 query heads:
+    68, 36 and 48 vectors), contexts that end mid-block, shuffled pages; one
+    workgroup per item or three KV splits merged by the combine kernel."""
+    monkeypatch.setenv("VX_ATTN_SHARED_SPLITS", splits)
+    rng = np.random.default_rng(100 + d)
+    rows, ps = [17, 9, 12], 16
+    offs = [501, 430, 515]
+    nb = (max(o + r for o, r in zip(offs, rows)) + ps - 1) // ps
+    P = 3 * nb + 2
+    perm = rng.permutation(P)[: 3 * nb].reshape(3, nb)
+    got, ref = _prefill_case(rows, offs, perm, P, 61 + d, dt=dt, hq=8, hk=2, d=d)
+    tol = 1e-2 if dt == "f16" else 3e-2
+    assert_allclose_elementwise(f"shared-kv d={d} {dt} splits={splits}", got, ref, tol, tol)
+
+
+@pytest.mark.parametrize("splits", ["1", "2"])
+def test_shared_kv_attention_tree_bf16(cuda, monkeypatch, splits):
+    """The 4-2-2 tree (68 vectors per KV head) in bf16 at d = 64, short
+    contexts (the tree slots dominate the key range)."""
+    monkeypatch.setenv("VX_ATTN_SHARED_SPLITS", splits)
+    par = tree_4_2_2()
+    R, B, ps = len(par), 3, 16
+    offs = [0, 5, 70]
+    nb = (max(offs) + R + ps - 1) // ps
+    rng = np.random.default_rng(12)
+    perm = rng.permutation(B * nb).reshape(B, nb)
+    got, ref = _prefill_case([R] * B, offs, perm, B * nb, 19, dt="bf16", hq=8, hk=2, d=64, tree=par)
+    assert_allclose_elementwise("shared-kv tree bf16", got, ref, 3e-2, 3e-2)
+
+
+def test_shared_kv_attention_sliding_window(cuda):
+    """Window 16 over 12 rows x 4 query heads (48 vectors, the shared-KV
+    kernel) at kv_offset 80: matches the oracle and differs from the global
+    result."""
+    from velox_amd import ops
+
+    hq, hk, d, ps, mb, p, window, R = 8, 2, 64, 16, 8, 8, 16, 12
+    scale = 1.0 / np.sqrt(d)
+    q = vxo.round_to(rand_vec(R * hq * d, 51), vxo.BF16).reshape(R, hq, d)
+    k = vxo.round_to(rand_vec(p * hk * ps * d, 52), vxo.BF16).reshape(p, hk, ps, d)
+    v = vxo.round_to(rand_vec(p * hk * ps * d, 53), vxo.BF16).reshape(p, hk, ps, d)
+    bt = np.arange(mb, dtype=np.uint32).reshape(1, mb)
+    cu, sid, kvo = np.array([0, R], np.uint32), np.zeros(R, np.uint32), np.array([80], np.uint32)
+    args = (dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(v, torch.bfloat16), u32(bt), u32(cu), u32(sid),
+            u32(kvo), scale)
+    swa = host(ops.paged_prefill_attention(*args, sliding_window=window))
+    glob = host(ops.paged_prefill_attention(*args))
+    cpu = vxo.paged_attention(q, k, v, bt, cu, kvo, scale, sliding_window=window)
+    assert_close("shared-kv swa", swa, cpu, 3e-2, 3e-2)
+    assert np.abs(glob - swa).max() > 1e-2, "the window did not change the output"
+
+
+def test_shared_kv_attention_matches_tiled(cuda, monkeypatch):
+    """Config 3's geometry through both kernels (shared-KV and the 32-vector
+    tiles, VX_ATTN_SHARED=0): the same attention up to f32 summation order."""
+    par = tree_4_2_2()
+    R, B, ps, ctx = len(par), 16, 16, 2048
+    nb = (ctx + R + ps - 1) // ps
+    rng = np.random.default_rng(34)
+    P = B * nb + 5
+    perm = rng.permutation(P)[: B * nb].reshape(B, nb)
+    shared, ref = _prefill_case([R] * B, [ctx] * B, perm, P, 304, dt="f16", hq=32, hk=8, tree=par)
+    monkeypatch.setenv("VX_ATTN_SHARED", "0")
+    tiled, _ = _prefill_case([R] * B, [ctx] * B, perm, P, 304, dt="f16", hq=32, hk=8, tree=par)
+    assert_allclose_elementwise("shared vs oracle", shared, ref, 1e-2, 1e-2)
+    assert_allclose_elementwise("tiled vs oracle", tiled, ref, 1e-2, 1e-2)
+    assert np.abs(shared.astype(np.float32) - tiled.astype(np.float32)).max() < 2e-3
+
+
 # ---------------------------------------------------------------- rope / scatter
 def test_rope_bf16_reference_case(cuda):
     from velox_amd import ops

@@ -54,6 +54,7 @@ struct AttnArgs {
     float scale_log2;               // scale * log2(e)
     uint32_t window;
     int out_bf16_round;  // round the output to bf16 before the 16-bit store
+    int pnv;             // query vectors per split partial (attn_combine_kernel)
     // Fused qkv finish (mode 0, one query tile per sequence): with qkv set,
     // the query vectors and the sequence's new K/V rows are formed here from
     // the qkv projection's f32 split partials [qkv_splits][total_q][N] --
@@ -540,42 +541,372 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const uint32_t *bt_arg,
     }
 }
 
-// Merge the split partials of one (sequence, kv-head, tile) in split order.
+// Shared-KV attention: one workgroup per (sequence, KV head, KV split) holds
+// all of the item's query vectors (its rows x G query heads, up to 128).  The
+// eight waves stage each 64-key block once in LDS -- K row-major with its
+// 16-byte chunks XOR-swizzled by row, V transposed (d-major, keys in pairs
+// per 32-bit word) -- and wave w runs query tile w (vectors 16 w .. 16 w + 15)
+// over every block of the range, with the S^T / P^T / O^T fragment layouts of
+// paged_attn_kernel.  The tiled kernel reads an item's KV range once per
+// query tile; a 17-node tree with 4 query heads per KV head has 68 vectors,
+// i.e. three 32-vector tiles and three reads.  Block b + 1 is requested into
+// registers while block b is computed, and the block table one block ahead
+// of that.  Keys past the range are staged as zeros.  Splits publish
+// (m, l, O) for attn_combine_kernel with kSharedNV vectors per partial.
+constexpr int kSharedWaves = 8;
+constexpr int kSharedNV = kSharedWaves * 16;
+
+template <int KT, int D>
+constexpr size_t attn_shared_lds_bytes() {
+    return 2 * ((size_t)kKeyBlock * D * 2 + (size_t)D * (kKeyBlock + 4) * 2);
+}
+
+template <int KT, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 2))) void paged_attn_shared_kernel(const uint32_t *bt_arg, const uint32_t *cu_arg,
+                                                                const uint32_t *kvo_arg, int n_splits_arg,
+                                                                int h_kv_arg, int max_blocks_arg, int chunk_arg,
+                                                                int ps_arg, AttnArgs a) {
+    typedef typename MfmaT<KT>::frag frag;
+    constexpr int DK = D / 32;               // MFMA k-steps over head_dim
+    constexpr int DT = D / 16;               // output row tiles of O^T
+    constexpr int CH = D / 8;                // 16-byte chunks per K/V row
+    constexpr int VT_STRIDE = kKeyBlock + 4;  // halves per transposed V row
+    constexpr int KBYTES = kKeyBlock * D * 2;
+    constexpr int BUFBYTES = KBYTES + D * VT_STRIDE * 2;
+    constexpr int NT = 64 * kSharedWaves;          // threads
+    constexpr int KC = (kKeyBlock * CH + NT - 1) / NT;  // K chunks per thread and block
+    constexpr int VC = (32 * CH + NT - 1) / NT;         // V (key pair, chunk) units per thread and block
+    __shared__ __attribute__((aligned(16))) unsigned char smem[attn_shared_lds_bytes<KT, D>()];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int lq = lane & 15;
+    const int lg = lane >> 4;
+    const int split = blockIdx.x % n_splits_arg;
+    const int item = blockIdx.x / n_splits_arg;
+    const int hk = item % h_kv_arg;
+    const int seq = item / h_kv_arg;
+
+    const int row0 = (int)cu_arg[seq];
+    const int r_seq = (int)cu_arg[seq + 1] - row0;
+    const int off = (int)kvo_arg[seq];
+    const int nq = r_seq * a.G;  // live query vectors (<= kSharedNV, checked by the launcher)
+    if (nq <= 0) return;         // uniform over the workgroup, before any barrier
+    const int kv_end = off + r_seq;
+    const int k_lo = split * chunk_arg;
+    const int k_hi = min(kv_end, k_lo + chunk_arg);
+    const int nb = k_hi > k_lo ? (k_hi - k_lo + kKeyBlock - 1) / kKeyBlock : 0;
+    const bool busy = wave * 16 < nq;  // this wave has a query tile
+
+    const uint32_t *btr = bt_arg + (int64_t)seq * max_blocks_arg;
+    const int64_t head_stride = (int64_t)ps_arg * D;
+    const int64_t page_stride = (int64_t)a.h_kv * head_stride;
+    const uint16_t *kbase = (const uint16_t *)a.k + hk * head_stride;
+    const uint16_t *vbase = (const uint16_t *)a.v + hk * head_stride;
+
+    // staging units of this thread: K chunk idx = tid + NT j (key idx / CH,
+    // chunk idx % CH); V unit idx = tid + NT j (key pair idx / CH, chunk
+    // idx % CH).  Both are row-major over the lanes of a wave, so each load
+    // instruction reads whole rows.
+    auto kkey = [&](int j) { return (tid + NT * j) / CH; };
+    auto kchk = [&](int j) { return (tid + NT * j) % CH; };
+    auto vpair = [&](int j) { return (tid + NT * j) / CH; };
+    auto vchk = [&](int j) { return (tid + NT * j) % CH; };
+    auto klive = [&](int j) { return tid + NT * j < kKeyBlock * CH; };
+    auto vlive = [&](int j) { return tid + NT * j < 32 * CH; };
+    auto page_of = [&](int key) {
+        return min(btr[min(key / ps_arg, max_blocks_arg - 1)], (uint32_t)(a.num_pages - 1));
+    };
+
+    uint32_t kpg[KC], vpg[VC][2];
+    uint4 kr[KC], vr[VC][2];
+    auto lookup = [&](int b) {  // pages of this thread's staging keys of block b
+        const int kb = k_lo + b * kKeyBlock;
+#pragma unroll
+        for (int j = 0; j < KC; j++) kpg[j] = klive(j) ? page_of(kb + kkey(j)) : 0u;
+#pragma unroll
+        for (int j = 0; j < VC; j++) {
+            vpg[j][0] = vlive(j) ? page_of(kb + 2 * vpair(j)) : 0u;
+            vpg[j][1] = vlive(j) ? page_of(kb + 2 * vpair(j) + 1) : 0u;
+        }
+    };
+    auto request = [&](int b) {  // K/V rows of block b into registers (zeros past the range)
+        const int kb = k_lo + b * kKeyBlock;
+#pragma unroll
+        for (int j = 0; j < KC; j++) {
+            const int key = kb + kkey(j);
+            kr[j] = make_uint4(0u, 0u, 0u, 0u);
+            if (klive(j) && key < k_hi)
+                kr[j] = *(const uint4 *)(kbase + (int64_t)kpg[j] * page_stride + (int64_t)(key % ps_arg) * D +
+                                         8 * kchk(j));
+        }
+#pragma unroll
+        for (int j = 0; j < VC; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int key = kb + 2 * vpair(j) + h;
+                vr[j][h] = make_uint4(0u, 0u, 0u, 0u);
+                if (vlive(j) && key < k_hi)
+                    vr[j][h] = *(const uint4 *)(vbase + (int64_t)vpg[j][h] * page_stride +
+                                                (int64_t)(key % ps_arg) * D + 8 * vchk(j));
+            }
+    };
+    auto stage = [&](int buf) {  // registers -> LDS buffer
+        unsigned char *kb_s = smem + buf * BUFBYTES;
+        uint16_t *vt = (uint16_t *)(kb_s + KBYTES);
+#pragma unroll
+        for (int j = 0; j < KC; j++)
+            if (klive(j)) {
+                const int key = kkey(j);
+                *(uint4 *)(kb_s + (key * CH + (kchk(j) ^ (key & (CH - 1)))) * 16) = kr[j];
+            }
+#pragma unroll
+        for (int j = 0; j < VC; j++)
+            if (vlive(j)) {
+                const uint32_t a0[4] = {vr[j][0].x, vr[j][0].y, vr[j][0].z, vr[j][0].w};
+                const uint32_t a1[4] = {vr[j][1].x, vr[j][1].y, vr[j][1].z, vr[j][1].w};
+                uint32_t *dst = (uint32_t *)(vt + 8 * vchk(j) * VT_STRIDE + 2 * vpair(j));
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    dst[(2 * e) * (VT_STRIDE / 2)] = (a0[e] & 0xffffu) | (a1[e] << 16);
+                    dst[(2 * e + 1) * (VT_STRIDE / 2)] = (a0[e] >> 16) | (a1[e] & 0xffff0000u);
+                }
+            }
+    };
+
+    // ---- this wave's query tile: vector n = 16 wave + lq, row t0 + n / G
+    frag qf[DK];
+    const int n = wave * 16 + lq;
+    const bool qlive = n < nq;
+    const int tq = n / a.G;
+    const int q_row = qlive ? row0 + tq : -1;
+    const uint64_t q_mask = (qlive && a.tmask) ? a.tmask[row0 + tq] : 0ull;
+    const int q_lim = qlive ? off + tq + 1 : 0;
+    const int hq = hk * a.G + (n % a.G);
+#pragma unroll
+    for (int ks = 0; ks < DK; ks++) {
+        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+        if (qlive) raw = *(const uint4 *)((const uint16_t *)a.q + ((int64_t)q_row * a.h_q + hq) * D + ks * 32 + lg * 8);
+        qf[ks] = __builtin_bit_cast(frag, raw);
+    }
+    const int win = (int)a.window;
+    const int hi_q = q_row < 0 ? 0 : min(k_hi, a.tmask ? kv_end : q_lim);
+    const int lo_q = (win > 0 && q_lim > win) ? q_lim - win : 0;
+
+    floatx4 o[DT];
+#pragma unroll
+    for (int i = 0; i < DT; i++) o[i] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    float m_run = -__builtin_inff(), l_run = 0.f;
+
+    if (nb > 0) {
+        lookup(0);
+        request(0);
+        if (nb > 1) lookup(1);
+    }
+    for (int b = 0; b < nb; b++) {
+        const int buf = b & 1;
+        stage(buf);
+        __syncthreads();  // block b staged; every wave is past block b - 1
+        if (b + 1 < nb) {
+            request(b + 1);
+            if (b + 2 < nb) lookup(b + 2);
+        }
+        if (!busy) continue;
+        const unsigned char *ks_s = smem + buf * BUFBYTES;
+        const uint16_t *vt = (const uint16_t *)(ks_s + KBYTES);
+        const int kb = k_lo + b * kKeyBlock;
+        // ---- S^T = K . Q^T
+        floatx4 s[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const int key = mt * 16 + lq;
+            floatx4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < DK; ks++) {
+                const uint4 raw = *(const uint4 *)(ks_s + (key * CH + ((ks * 4 + lg) ^ (key & (CH - 1)))) * 16);
+                c = MfmaT<KT>::mma(__builtin_bit_cast(frag, raw), qf[ks], c);
+            }
+            s[mt] = c;
+            // one 16-key tile of K fragments live at a time (register budget
+            // of four waves per SIMD)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // ---- mask, scale, block max (the rules of paged_attn_kernel)
+        float bmax = -__builtin_inff();
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = kb + mt * 16 + lg * 4 + r;
+                bool vis = key >= lo_q && key < hi_q;
+                if (a.tmask && key >= off) vis = vis && (key - off) < 64 && ((q_mask >> (key - off)) & 1ull);
+                const float v = vis ? s[mt][r] * a.scale_log2 : -__builtin_inff();
+                s[mt][r] = v;
+                bmax = fmaxf(bmax, v);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        // ---- probabilities, running stats, rescale O
+        const float m_new = fmaxf(m_run, bmax);
+        const bool dead = m_new == -__builtin_inff();
+        const float alpha = dead ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        float psum = 0.f;
+        uint16_t ph[4][4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = dead ? 0.f : __builtin_amdgcn_exp2f(s[mt][r] - m_new);
+                psum += p;
+                ph[mt][r] = MfmaT<KT>::cvt(p);
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int i = 0; i < DT; i++) o[i] *= alpha;
+        frag pf[2];
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            unsigned short tmp[8] __attribute__((aligned(16)));
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                tmp[r] = ph[2 * st][r];
+                tmp[4 + r] = ph[2 * st + 1][r];
+            }
+            pf[st] = *(frag *)tmp;
+        }
+        // ---- O^T += V^T . P^T ; A element e <-> key 32*st + 4*lg + (e < 4 ? e : 12 + e)
+#pragma unroll
+        for (int i = 0; i < DT; i++) {
+            const uint16_t *vrow = vt + (i * 16 + lq) * VT_STRIDE;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const uint2 lo = *(const uint2 *)(vrow + st * 32 + lg * 4);
+                const uint2 hi = *(const uint2 *)(vrow + st * 32 + 16 + lg * 4);
+                const frag vf = __builtin_bit_cast(frag, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                o[i] = MfmaT<KT>::mma(vf, pf[st], o[i]);
+            }
+            if (i % 2 == 1) __builtin_amdgcn_sched_barrier(0);  // bounds the V^T fragments in flight
+        }
+    }
+    if (!busy) return;
+
+    const int64_t item_id = (int64_t)seq * a.h_kv + hk;
+    if (n_splits_arg > 1) {
+        // partial layout per (item, split): m[NV], l[NV], O[NV][D]
+        float *pbase = a.partial + (item_id * n_splits_arg + split) * (int64_t)(2 * kSharedNV + kSharedNV * D);
+        if (lg == 0) {
+            pbase[n] = m_run;
+            pbase[kSharedNV + n] = l_run;
+        }
+#pragma unroll
+        for (int i = 0; i < DT; i++)
+            *(float4 *)(pbase + 2 * kSharedNV + (int64_t)n * D + i * 16 + lg * 4) =
+                make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+        return;
+    }
+    if (!qlive) return;
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int i = 0; i < DT; i++) {
+        uint16_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float val = o[i][r] * inv;
+            if (a.out_bf16_round) val = round_to<VX_BF16>(val);
+            h[r] = MfmaT<KT>::cvt(val);
+        }
+        const int64_t oi = ((int64_t)q_row * a.h_q + hq) * D + i * 16 + lg * 4;
+        *(uint2 *)((uint16_t *)a.out + oi) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                                        (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+    }
+}
+
+// Merge the split partials of each (sequence, kv-head, tile) in split order;
+// a partial holds a.pnv vectors: m[pnv], l[pnv], O[pnv][D].  One thread per
+// (tile, vector, four consecutive d), nv vectors per tile; the splits'
+// statistics and values are requested eight splits at a time, so a merge of
+// up to eight splits costs two memory round trips.
 template <int KT>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    int item = blockIdx.x;
-    const int qtile = item % a.n_qtiles;
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int nv) {
+    constexpr int kB = 8;
+    const int D4 = a.D / 4;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_tile = (int64_t)nv * D4;
+    int64_t item = gid / per_tile;
+    const int rem = (int)(gid - item * per_tile);
+    const int n = rem / D4;
+    const int d = (rem - n * D4) * 4;
+    const int qtile = (int)(item % a.n_qtiles);
     item /= a.n_qtiles;
-    const int hk = item % a.h_kv;
-    const int seq = item / a.h_kv;
+    const int hk = (int)(item % a.h_kv);
+    const int seq = (int)(item / a.h_kv);
+    if (seq >= a.n_seqs) return;
     int r_seq, row0, off;
     row_info(a, seq, r_seq, row0, off);
     if (a.mode == 1 && (int)a.kvo[seq] == 0) r_seq = 0;
     const int t0 = qtile * a.qr;
     if (t0 >= r_seq) return;
     const int nq = (min(r_seq, t0 + a.qr) - t0) * a.G;
+    if (n >= nq) return;
     const int64_t tile_id = ((int64_t)seq * a.h_kv + hk) * a.n_qtiles + qtile;
-    const int64_t stride = 128 + 64 * (int64_t)a.D;
+    const int64_t stride = (int64_t)a.pnv * (2 + a.D);
     const float *p0 = a.partial + tile_id * a.n_splits * stride;
-    for (int e = threadIdx.x; e < nq * a.D; e += blockDim.x) {
-        const int n = e / a.D;
-        const int d = e - n * a.D;
-        float M = -__builtin_inff();
-        for (int sp = 0; sp < a.n_splits; sp++) M = fmaxf(M, p0[sp * stride + n]);
-        float L = 0.f, acc = 0.f;
-        for (int sp = 0; sp < a.n_splits; sp++) {
-            const float *ps = p0 + sp * stride;
-            const float ms = ps[n];
-            const float f = ms == -__builtin_inff() ? 0.f : exp2f(ms - M);
-            L += ps[64 + n] * f;
-            acc += ps[128 + (int64_t)n * a.D + d] * f;
-        }
-        float val = acc / L;
-        if (a.out_bf16_round) val = round_to<VX_BF16>(val);
-        const int t = t0 + n / a.G;
-        const int hq = hk * a.G + (n % a.G);
-        ((uint16_t *)a.out)[((int64_t)(row0 + t) * a.h_q + hq) * a.D + d] = MfmaT<KT>::cvt(val);
+    float M = -__builtin_inff();
+    for (int s0 = 0; s0 < a.n_splits; s0 += kB) {
+        float mb[kB];
+#pragma unroll
+        for (int j = 0; j < kB; j++) mb[j] = s0 + j < a.n_splits ? p0[(s0 + j) * stride + n] : -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < kB; j++) M = fmaxf(M, mb[j]);
     }
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < a.n_splits; s0 += kB) {
+        float mb[kB], lb[kB];
+        float4 ob[kB];
+#pragma unroll
+        for (int j = 0; j < kB; j++) {
+            const bool ok = s0 + j < a.n_splits;
+            const float *ps = p0 + (int64_t)(s0 + j) * stride;
+            mb[j] = ok ? ps[n] : -__builtin_inff();
+            lb[j] = ok ? ps[a.pnv + n] : 0.f;
+            ob[j] = ok ? *(const float4 *)(ps + 2 * a.pnv + (int64_t)n * a.D + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < kB; j++) {
+            if (s0 + j >= a.n_splits) break;
+            const float f = mb[j] == -__builtin_inff() ? 0.f : exp2f(mb[j] - M);
+            L += lb[j] * f;
+            acc.x += ob[j].x * f;
+            acc.y += ob[j].y * f;
+            acc.z += ob[j].z * f;
+            acc.w += ob[j].w * f;
+        }
+    }
+    const float vals[4] = {acc.x / L, acc.y / L, acc.z / L, acc.w / L};
+    uint16_t h[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float val = vals[r];
+        if (a.out_bf16_round) val = round_to<VX_BF16>(val);
+        h[r] = MfmaT<KT>::cvt(val);
+    }
+    const int t = t0 + n / a.G;
+    const int hq = hk * a.G + (n % a.G);
+    *(uint2 *)((uint16_t *)a.out + ((int64_t)(row0 + t) * a.h_q + hq) * a.D + d) =
+        make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+}
+
+void launch_combine(const AttnArgs &a, int dtype, int64_t n_tiles, int nv, hipStream_t st) {
+    const unsigned grid = (unsigned)vx_cdiv(n_tiles * nv * (a.D / 4), 256);
+    if (dtype == VX_F16)
+        hipLaunchKernelGGL(attn_combine_kernel<VX_F16>, dim3(grid), dim3(256), 0, st, a, nv);
+    else
+        hipLaunchKernelGGL(attn_combine_kernel<VX_BF16>, dim3(grid), dim3(256), 0, st, a, nv);
 }
 
 // Plain per-(row, q-head) kernel, the reference's loop (MSL :307-395 / :107-191)
@@ -668,11 +999,62 @@ int dispatch_attn(const AttnArgs &a, int QT, int64_t n_items, hipStream_t st) {
     return set_error("paged_attention: no kernel for head_dim");
 }
 
+template <int KT>
+int dispatch_attn_shared(const AttnArgs &a, int64_t n_items, hipStream_t st) {
+#define VX_SCASE(d)                                                                                              \
+    if (a.D == d) {                                                                                              \
+        hipLaunchKernelGGL((paged_attn_shared_kernel<KT, d>), dim3((unsigned)n_items), dim3(64 * kSharedWaves), 0, \
+                           st, a.bt, a.cu, a.kvo, a.n_splits, a.h_kv, a.max_blocks, a.chunk, a.ps, a);           \
+        return 0;                                                                                                \
+    }
+    VX_SCASE(32) VX_SCASE(64) VX_SCASE(128) VX_SCASE(256)
+#undef VX_SCASE
+    return set_error("paged_attention: no kernel for head_dim");
+}
+
+// The shared-KV kernel takes a sequence's query vectors when they exceed one
+// 32-vector tile and fit its eight waves (mode 0, 16-bit, no fused qkv
+// finish); VX_ATTN_SHARED=0 turns it off.
+bool use_shared_attn(int mode, int64_t max_rows, int64_t G, int64_t D) {
+    const char *env = getenv("VX_ATTN_SHARED");
+    if (env && env[0] == '0') return false;
+    const int64_t v = max_rows * G;
+    return mode == 0 && v > 32 && v <= kSharedNV && (D == 32 || D == 64 || D == 128 || D == 256);
+}
+
+// Its KV split: ~2 workgroups per CU (one at D = 256, whose LDS fills a CU),
+// at least two key blocks per split.  VX_ATTN_SHARED_SPLITS overrides the count.
+void shared_attn_plan(int64_t base_items, int64_t max_kv, int64_t D, int64_t &splits, int64_t &chunk) {
+    const int64_t max_keys = std::max<int64_t>(1, max_kv);
+    const int64_t per_cu = D <= 128 ? 2 : 1;
+    splits = std::max<int64_t>(1, per_cu * device_cu_count() / std::max<int64_t>(1, base_items));
+    const char *env = getenv("VX_ATTN_SHARED_SPLITS");
+    if (env && *env) splits = std::max(1, atoi(env));
+    chunk = vx_cdiv(vx_cdiv(max_keys, splits), kKeyBlock) * kKeyBlock;
+    chunk = std::max<int64_t>(chunk, 2 * kKeyBlock);
+    splits = vx_cdiv(max_keys, chunk);
+}
+
 }  // namespace
 
 size_t attn_workspace_bytes(int64_t n_seqs, int64_t h_kv, int64_t n_qtiles, int64_t n_splits, int64_t D) {
     if (n_splits <= 1) return kAttnCounterBytes;
     return kAttnCounterBytes + (size_t)n_seqs * h_kv * n_qtiles * n_splits * (128 + 64 * D) * 4;
+}
+
+// Upper bound of the workspace paged_attention_launch needs for any batch
+// within these limits (either kernel, splits of at least 128 keys).
+size_t attn_workspace_bound(int64_t n_seqs, int64_t h_kv, int64_t max_rows, int64_t G, int64_t D, int64_t max_kv) {
+    const int64_t qn_max = D <= 128 ? 64 : 32;
+    int64_t qt = std::max<int64_t>(1, vx_cdiv(std::min<int64_t>(max_rows * G, qn_max), 16));
+    if (qt == 3) qt = 4;
+    const int64_t qr = std::max<int64_t>(1, qt * 16 / G);
+    const int64_t nqt = vx_cdiv(max_rows, qr);
+    const int64_t splits = std::max<int64_t>(1, vx_cdiv(max_kv, 2 * kKeyBlock));
+    size_t need = attn_workspace_bytes(n_seqs, h_kv, nqt, splits, D);
+    if (use_shared_attn(0, max_rows, G, D) && splits > 1)
+        need = std::max(need, kAttnCounterBytes + (size_t)n_seqs * h_kv * splits * kSharedNV * (2 + D) * 4);
+    return need;
 }
 
 // Shared launcher for the C ABI and the engine.
@@ -727,6 +1109,35 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
         VX_HIP(hipGetLastError());
         return 0;
     }
+    a.pnv = 64;
+    if (use_shared_attn(mode, max_rows, a.G, D) && !fuse) {
+        // one workgroup per (sequence, KV head, split) over all query vectors
+        const int64_t base_items = n_seqs * h_kv;
+        int64_t splits, chunk;
+        shared_attn_plan(base_items, max_kv, D, splits, chunk);
+        a.n_qtiles = 1;
+        a.qr = (int)max_rows;
+        a.pnv = kSharedNV;
+        a.chunk = (int)chunk;
+        a.n_splits = (int)splits;
+        void *ws = workspace;
+        const size_t need = kAttnCounterBytes + (size_t)base_items * splits * kSharedNV * (2 + D) * 4;
+        if (splits > 1) {
+            if (!ws) {
+                VX_TRY(stream_workspace(st, need, &ws));
+            } else if (ws_bytes < need) {
+                return set_error("paged_attention: workspace too small");
+            }
+        }
+        a.partial = ws ? (float *)((char *)ws + kAttnCounterBytes) : nullptr;
+        const int64_t n_items = base_items * splits;
+        int rc = dtype == VX_F16 ? dispatch_attn_shared<VX_F16>(a, n_items, st)
+                                 : dispatch_attn_shared<VX_BF16>(a, n_items, st);
+        if (rc) return rc;
+        if (splits > 1) launch_combine(a, dtype, base_items, (int)std::min<int64_t>(kSharedNV, max_rows * a.G), st);
+        VX_HIP(hipGetLastError());
+        return 0;
+    }
     // Query vectors per tile.  Every query tile reads the sequence's whole KV
     // range, and the 64-vector tile is a heavy kernel (one workgroup per CU).
     // When a sequence's queries need two 64-vector tiles anyway (65..128, e.g.
@@ -775,12 +1186,7 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
     const int64_t n_items = base_items * splits;
     int rc = dtype == VX_F16 ? dispatch_attn<VX_F16>(a, QT, n_items, st) : dispatch_attn<VX_BF16>(a, QT, n_items, st);
     if (rc) return rc;
-    if (splits > 1) {
-        if (dtype == VX_F16)
-            hipLaunchKernelGGL(attn_combine_kernel<VX_F16>, dim3((unsigned)base_items), dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL(attn_combine_kernel<VX_BF16>, dim3((unsigned)base_items), dim3(256), 0, st, a);
-    }
+    if (splits > 1) launch_combine(a, dtype, base_items, std::min(64, a.qr * a.G), st);
     VX_HIP(hipGetLastError());
     return 0;
 }
@@ -813,12 +1219,15 @@ extern "C" int vx_paged_attention(const void *q, const void *k_pool, const void 
     // The reference's kernel finds a row's sequence through seq_id_per_q and
     // its position through cu_seqlens (MSL :307-395); this kernel walks the
     // cu_seqlens ranges, so the two must describe the same rows.  They are
-    // checked on the host (one small copy and a stream synchronisation).
+    // checked on the host (one small copy and a stream synchronisation), which
+    // also gives the launch plan the longest row range and key range.
+    int64_t max_rows = 1, max_kv = 1;
     {
         hipStream_t st = (hipStream_t)stream;
-        std::vector<uint32_t> cu((size_t)n_seqs + 1), sid((size_t)total_q);
+        std::vector<uint32_t> cu((size_t)n_seqs + 1), sid((size_t)total_q), kvo((size_t)n_seqs);
         VX_HIP(hipMemcpyAsync(cu.data(), cu_seqlens, cu.size() * 4, hipMemcpyDeviceToHost, st));
         VX_HIP(hipMemcpyAsync(sid.data(), seq_id_per_q, sid.size() * 4, hipMemcpyDeviceToHost, st));
+        VX_HIP(hipMemcpyAsync(kvo.data(), kv_offsets, kvo.size() * 4, hipMemcpyDeviceToHost, st));
         VX_HIP(hipStreamSynchronize(st));
         VX_REQUIRE(cu[0] == 0 && (int64_t)cu[n_seqs] == total_q, "paged_attention: cu_seqlens must run from 0 to total_q");
         for (int64_t s = 0; s < n_seqs; s++)
@@ -828,12 +1237,17 @@ extern "C" int vx_paged_attention(const void *q, const void *k_pool, const void 
             VX_REQUIRE(sq < (uint64_t)n_seqs && cu[sq] <= (uint64_t)row && (uint64_t)row < cu[sq + 1],
                        "paged_attention: seq_id_per_q[" + std::to_string(row) + "] disagrees with cu_seqlens");
         }
+        for (int64_t s = 0; s < n_seqs; s++) {
+            const int64_t r = (int64_t)cu[s + 1] - cu[s];
+            max_rows = std::max(max_rows, r);
+            max_kv = std::max(max_kv, (int64_t)kvo[s] + r);
+        }
+        max_kv = std::min(max_kv, max_blocks * page_size);  // the block table bounds the key range
     }
-    // rows per sequence and KV length are bounded by total_q and the block table
     return paged_attention_launch(q, k_pool, v_pool, block_table, cu_seqlens, kv_offsets, tree_mask,
-                                  out, 0, total_q, n_seqs, total_q, max_blocks, num_pages, h_q, h_kv,
+                                  out, 0, total_q, n_seqs, max_rows, max_blocks, num_pages, h_q, h_kv,
                                   head_dim, page_size, scale, sliding_window, dtype, nullptr, 0,
-                                  max_blocks * page_size, (hipStream_t)stream, 0, nullptr);
+                                  max_kv, (hipStream_t)stream, 0, nullptr);
 }
 
 extern "C" int vx_paged_decode_attention(const void *q, const void *k_pool, const void *v_pool,

@@ -104,7 +104,7 @@ int qmm_packed(const void *x, const void *packed, void *y, const void *resid, in
                int x_shift, int y_shift, int round_dt, int y_dt, int epi, void *workspace, size_t ws_bytes,
                hipStream_t st);
 size_t qmm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epi, bool packed);
-size_t attn_workspace_bytes(int64_t n_seqs, int64_t h_kv, int64_t n_qtiles, int64_t n_splits, int64_t D);
+size_t attn_workspace_bound(int64_t n_seqs, int64_t h_kv, int64_t max_rows, int64_t G, int64_t D, int64_t max_kv);
 int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool, const uint32_t *bt,
                            const uint32_t *cu, const uint32_t *kvo, const uint64_t *tmask, void *out,
                            int mode, int64_t total_q, int64_t n_seqs, int64_t max_rows,
@@ -742,15 +742,9 @@ size_t forward_ws_bytes(const vx_model *m, int64_t rows, int64_t logit_rows, int
     need = std::max(need, qmm_partial_ws_bytes(rows, H, F));
     need = std::max(need, qmm_workspace_bytes(logit_rows, c.vocab, H, VX_EPI_STORE, true));
     // attention: upper bound on its split plan (see paged_attention_launch)
-    const int64_t G = c.n_heads / c.n_kv_heads;
-    const int64_t qn_max = c.head_dim <= 128 ? 64 : 32;
-    int64_t qt = std::max<int64_t>(1, vx_cdiv(std::min<int64_t>(max_rows * G, qn_max), 16));
-    if (qt == 3) qt = 4;
-    const int64_t qr = std::max<int64_t>(1, qt * 16 / G);
-    const int64_t nqt = vx_cdiv(max_rows, qr);
-    const int64_t splits = std::max<int64_t>(1, vx_cdiv(max_kv, 128));
     need = std::max(need, attn_ws_offset(rows, QW + 2 * KW, H) +
-                              attn_workspace_bytes(n_seqs, c.n_kv_heads, nqt, splits, c.head_dim));
+                              attn_workspace_bound(n_seqs, c.n_kv_heads, max_rows, c.n_heads / c.n_kv_heads,
+                                                   c.head_dim, max_kv));
     return need;
 }
 
