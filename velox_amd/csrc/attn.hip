@@ -716,15 +716,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
         const unsigned char *ks_s = smem + buf * BUFBYTES;
         const uint16_t *vt = (const uint16_t *)(ks_s + KBYTES);
         const int kb = k_lo + b * kKeyBlock;
-        // ---- S^T = K . Q^T
+        // ---- S^T = K . Q^T; row mt*16 + lq = (mt*16) | lq, so its swizzle is
+        // (lq ^ (mt*16)) & (CH-1) and the tile offset an immediate
         floatx4 s[4];
 #pragma unroll
         for (int mt = 0; mt < 4; mt++) {
-            const int key = mt * 16 + lq;
             floatx4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < DK; ks++) {
-                const uint4 raw = *(const uint4 *)(ks_s + (key * CH + ((ks * 4 + lg) ^ (key & (CH - 1)))) * 16);
+                const int chunk = ((ks * 4 + lg) ^ lq ^ (mt * 16)) & (CH - 1);
+                const uint4 raw = *(const uint4 *)(ks_s + mt * 16 * CH * 16 + lq * CH * 16 + chunk * 16);
                 c = MfmaT<KT>::mma(__builtin_bit_cast(frag, raw), qf[ks], c);
             }
             s[mt] = c;
@@ -732,19 +733,49 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
             // of four waves per SIMD)
             __builtin_amdgcn_sched_barrier(0);
         }
-        // ---- mask, scale, block max (the rules of paged_attn_kernel)
+        // ---- mask, scale, block max (the rules of paged_attn_kernel).  A
+        // block of context keys wholly inside the range, below the first
+        // query row and with no window is visible to every query (the
+        // workgroup-uniform fast path); otherwise the rules are evaluated
+        // per score without branches.
         float bmax = -__builtin_inff();
+        if (win == 0 && kb + kKeyBlock <= off && kb + kKeyBlock <= k_hi) {
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++)
+            for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int key = kb + mt * 16 + lg * 4 + r;
-                bool vis = key >= lo_q && key < hi_q;
-                if (a.tmask && key >= off) vis = vis && (key - off) < 64 && ((q_mask >> (key - off)) & 1ull);
-                const float v = vis ? s[mt][r] * a.scale_log2 : -__builtin_inff();
-                s[mt][r] = v;
-                bmax = fmaxf(bmax, v);
+                for (int r = 0; r < 4; r++) {
+                    s[mt][r] *= a.scale_log2;
+                    bmax = fmaxf(bmax, s[mt][r]);
+                }
+        } else {
+            // tree rule as a word over the block's keys (bit j: key kb + j):
+            // context keys before off are visible, tree slot key - off per the
+            // row's ancestor bits, keys past the 64 slots not; then shifted so
+            // that this lane's element (mt, r) is bit 16 mt + r
+            uint64_t tv = ~0ull;
+            if (a.tmask) {
+                const int dd = kb - off;  // workgroup-uniform
+                if (dd >= 64)
+                    tv = 0ull;
+                else if (dd >= 0)
+                    tv = q_mask >> dd;
+                else if (dd > -64)
+                    tv = (q_mask << (-dd)) | ((1ull << (-dd)) - 1ull);
+                tv >>= lg * 4;
             }
+            const uint32_t tlo = (uint32_t)tv, thi = (uint32_t)(tv >> 32);
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = kb + mt * 16 + lg * 4 + r;
+                    const uint32_t bit = ((mt < 2 ? tlo : thi) >> ((mt & 1) * 16 + r)) & 1u;
+                    const bool vis = (key >= lo_q) & (key < hi_q) & (bit != 0u);
+                    const float v = vis ? s[mt][r] * a.scale_log2 : -__builtin_inff();
+                    s[mt][r] = v;
+                    bmax = fmaxf(bmax, v);
+                }
+        }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
         // ---- probabilities, running stats, rescale O
