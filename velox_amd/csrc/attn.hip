@@ -553,6 +553,15 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const uint32_t *bt_arg,
 // registers while block b is computed, and the block table one block ahead
 // of that.  Keys past the range are staged as zeros.  Splits publish
 // (m, l, O) for attn_combine_kernel with kSharedNV vectors per partial.
+// Workgroup barrier that orders LDS only: __syncthreads() is also a release
+// of global memory, i.e. a vmcnt(0) wait, which would drain the key blocks
+// requested ahead of it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 constexpr int kSharedWaves = 8;
 constexpr int kSharedNV = kSharedWaves * 16;
 
@@ -561,8 +570,8 @@ constexpr size_t attn_shared_lds_bytes() {
     return 2 * ((size_t)kKeyBlock * D * 2 + (size_t)D * (kKeyBlock + 4) * 2);
 }
 
-template <int KT, int D>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 2))) void paged_attn_shared_kernel(const uint32_t *bt_arg, const uint32_t *cu_arg,
+template <int KT, int D, int PF>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 && PF == 1 ? 4 : 2))) void paged_attn_shared_kernel(const uint32_t *bt_arg, const uint32_t *cu_arg,
                                                                 const uint32_t *kvo_arg, int n_splits_arg,
                                                                 int h_kv_arg, int max_blocks_arg, int chunk_arg,
                                                                 int ps_arg, AttnArgs a) {
@@ -615,57 +624,67 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     auto vchk = [&](int j) { return (tid + NT * j) % CH; };
     auto klive = [&](int j) { return tid + NT * j < kKeyBlock * CH; };
     auto vlive = [&](int j) { return tid + NT * j < 32 * CH; };
-    auto page_of = [&](int key) {
-        return min(btr[min(key / ps_arg, max_blocks_arg - 1)], (uint32_t)(a.num_pages - 1));
+    // Addressing (the launcher's precondition): a power-of-two page size, so
+    // key / ps and key % ps are shifts, and a pool of fewer than 2^31
+    // elements, so element offsets fit 32 bits.
+    const int lps = __builtin_ctz((unsigned)ps_arg);
+    // Block-table entries are loaded unconditionally (the index is clamped
+    // to the table row) and clamped to the pool where they are used: a use
+    // next to the load would make the compiler wait for every request in
+    // flight, the prefetched key blocks included.
+    auto page_of = [&](int key) { return btr[min(key >> lps, max_blocks_arg - 1)]; };
+    auto row_at = [&](const uint16_t *base, uint32_t page, int key, int chunk) {
+        page = min(page, (uint32_t)(a.num_pages - 1));
+        return *(const uint4 *)(base + (page * (uint32_t)page_stride + (uint32_t)((key & (ps_arg - 1)) * D + 8 * chunk)));
     };
 
-    uint32_t kpg[KC], vpg[VC][2];
-    uint4 kr[KC], vr[VC][2];
-    auto lookup = [&](int b) {  // pages of this thread's staging keys of block b
+    // a PF-slot ring: block b's rows and pages live in slot b % PF
+    uint32_t kpg[PF][KC], vpg[PF][VC][2];
+    uint4 kr[PF][KC], vr[PF][VC][2];
+    auto lookup = [&](int b, auto slot_c) __attribute__((always_inline)) {  // pages of this thread's staging keys of block b
+        constexpr int SL = decltype(slot_c)::value;
         const int kb = k_lo + b * kKeyBlock;
 #pragma unroll
-        for (int j = 0; j < KC; j++) kpg[j] = klive(j) ? page_of(kb + kkey(j)) : 0u;
+        for (int j = 0; j < KC; j++) kpg[SL][j] = page_of(kb + kkey(j));
 #pragma unroll
         for (int j = 0; j < VC; j++) {
-            vpg[j][0] = vlive(j) ? page_of(kb + 2 * vpair(j)) : 0u;
-            vpg[j][1] = vlive(j) ? page_of(kb + 2 * vpair(j) + 1) : 0u;
+            vpg[SL][j][0] = page_of(kb + 2 * vpair(j));
+            vpg[SL][j][1] = page_of(kb + 2 * vpair(j) + 1);
         }
     };
-    auto request = [&](int b) {  // K/V rows of block b into registers (zeros past the range)
+    auto request = [&](int b, auto slot_c) __attribute__((always_inline)) {  // K/V rows of block b into registers (zeros past the range)
+        constexpr int SL = decltype(slot_c)::value;
         const int kb = k_lo + b * kKeyBlock;
 #pragma unroll
         for (int j = 0; j < KC; j++) {
             const int key = kb + kkey(j);
-            kr[j] = make_uint4(0u, 0u, 0u, 0u);
-            if (klive(j) && key < k_hi)
-                kr[j] = *(const uint4 *)(kbase + (int64_t)kpg[j] * page_stride + (int64_t)(key % ps_arg) * D +
-                                         8 * kchk(j));
+            kr[SL][j] = make_uint4(0u, 0u, 0u, 0u);
+            if (klive(j) && key < k_hi) kr[SL][j] = row_at(kbase, kpg[SL][j], key, kchk(j));
         }
 #pragma unroll
         for (int j = 0; j < VC; j++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int key = kb + 2 * vpair(j) + h;
-                vr[j][h] = make_uint4(0u, 0u, 0u, 0u);
-                if (vlive(j) && key < k_hi)
-                    vr[j][h] = *(const uint4 *)(vbase + (int64_t)vpg[j][h] * page_stride +
-                                                (int64_t)(key % ps_arg) * D + 8 * vchk(j));
+                vr[SL][j][h] = make_uint4(0u, 0u, 0u, 0u);
+                if (vlive(j) && key < k_hi) vr[SL][j][h] = row_at(vbase, vpg[SL][j][h], key, vchk(j));
             }
     };
-    auto stage = [&](int buf) {  // registers -> LDS buffer
+    auto stage = [&](int buf, auto slot_c) __attribute__((always_inline)) {  // registers -> LDS buffer
+        constexpr int SL = decltype(slot_c)::value;
         unsigned char *kb_s = smem + buf * BUFBYTES;
         uint16_t *vt = (uint16_t *)(kb_s + KBYTES);
 #pragma unroll
         for (int j = 0; j < KC; j++)
             if (klive(j)) {
                 const int key = kkey(j);
-                *(uint4 *)(kb_s + (key * CH + (kchk(j) ^ (key & (CH - 1)))) * 16) = kr[j];
+                *(uint4 *)(kb_s + (key * CH + (kchk(j) ^ (key & (CH - 1)))) * 16) = kr[SL][j];
             }
 #pragma unroll
         for (int j = 0; j < VC; j++)
             if (vlive(j)) {
-                const uint32_t a0[4] = {vr[j][0].x, vr[j][0].y, vr[j][0].z, vr[j][0].w};
-                const uint32_t a1[4] = {vr[j][1].x, vr[j][1].y, vr[j][1].z, vr[j][1].w};
+                const uint32_t a0[4] = {vr[SL][j][0].x, vr[SL][j][0].y, vr[SL][j][0].z, vr[SL][j][0].w};
+                const uint32_t a1[4] = {vr[SL][j][1].x, vr[SL][j][1].y, vr[SL][j][1].z, vr[SL][j][1].w};
                 uint32_t *dst = (uint32_t *)(vt + 8 * vchk(j) * VT_STRIDE + 2 * vpair(j));
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -699,38 +718,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     for (int i = 0; i < DT; i++) o[i] = (floatx4){0.f, 0.f, 0.f, 0.f};
     float m_run = -__builtin_inff(), l_run = 0.f;
 
-    if (nb > 0) {
-        lookup(0);
-        request(0);
-        if (nb > 1) lookup(1);
-    }
-    for (int b = 0; b < nb; b++) {
+    // block b: its slot is staged into LDS buffer b & 1 (a barrier later every
+    // wave is past block b - 1, whose buffer block b + 1 overwrites), then the
+    // freed slot takes block b + PF and the next slot's pages block b + PF + 1
+    auto compute = [&](int b) __attribute__((always_inline)) {
         const int buf = b & 1;
-        stage(buf);
-        __syncthreads();  // block b staged; every wave is past block b - 1
-        if (b + 1 < nb) {
-            request(b + 1);
-            if (b + 2 < nb) lookup(b + 2);
-        }
-        if (!busy) continue;
         const unsigned char *ks_s = smem + buf * BUFBYTES;
         const uint16_t *vt = (const uint16_t *)(ks_s + KBYTES);
         const int kb = k_lo + b * kKeyBlock;
         // ---- S^T = K . Q^T; row mt*16 + lq = (mt*16) | lq, so its swizzle is
         // (lq ^ (mt*16)) & (CH-1) and the tile offset an immediate
+        // k-step outer: the four key tiles' products are independent, and
+        // one k-step of K fragments is live at a time (register budget of
+        // four waves per SIMD)
         floatx4 s[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
-            floatx4 c = {0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < 4; mt++) s[mt] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < DK; ks++) {
+        for (int ks = 0; ks < DK; ks++) {
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
                 const int chunk = ((ks * 4 + lg) ^ lq ^ (mt * 16)) & (CH - 1);
                 const uint4 raw = *(const uint4 *)(ks_s + mt * 16 * CH * 16 + lq * CH * 16 + chunk * 16);
-                c = MfmaT<KT>::mma(__builtin_bit_cast(frag, raw), qf[ks], c);
+                s[mt] = MfmaT<KT>::mma(__builtin_bit_cast(frag, raw), qf[ks], s[mt]);
             }
-            s[mt] = c;
-            // one 16-key tile of K fragments live at a time (register budget
-            // of four waves per SIMD)
             __builtin_amdgcn_sched_barrier(0);
         }
         // ---- mask, scale, block max (the rules of paged_attn_kernel).  A
@@ -796,8 +807,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
         psum += __shfl_xor(psum, 32);
         l_run = l_run * alpha + psum;
         m_run = m_new;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // a running max moved
 #pragma unroll
-        for (int i = 0; i < DT; i++) o[i] *= alpha;
+            for (int i = 0; i < DT; i++) o[i] *= alpha;
+        }
         frag pf[2];
 #pragma unroll
         for (int st = 0; st < 2; st++) {
@@ -810,19 +823,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
             pf[st] = *(frag *)tmp;
         }
         // ---- O^T += V^T . P^T ; A element e <-> key 32*st + 4*lg + (e < 4 ? e : 12 + e)
+        // key half outer: the d tiles' products are independent; four V^T
+        // fragments in flight at a time
 #pragma unroll
-        for (int i = 0; i < DT; i++) {
-            const uint16_t *vrow = vt + (i * 16 + lq) * VT_STRIDE;
+        for (int st = 0; st < 2; st++)
 #pragma unroll
-            for (int st = 0; st < 2; st++) {
+            for (int i = 0; i < DT; i++) {
+                const uint16_t *vrow = vt + (i * 16 + lq) * VT_STRIDE;
                 const uint2 lo = *(const uint2 *)(vrow + st * 32 + lg * 4);
                 const uint2 hi = *(const uint2 *)(vrow + st * 32 + 16 + lg * 4);
                 const frag vf = __builtin_bit_cast(frag, make_uint4(lo.x, lo.y, hi.x, hi.y));
                 o[i] = MfmaT<KT>::mma(vf, pf[st], o[i]);
+                if (i % 4 == 3) __builtin_amdgcn_sched_barrier(0);
             }
-            if (i % 2 == 1) __builtin_amdgcn_sched_barrier(0);  // bounds the V^T fragments in flight
-        }
+        };
+    auto iter = [&](int b, auto slot_c) __attribute__((always_inline)) {
+        constexpr int SL = decltype(slot_c)::value;
+        stage(b & 1, slot_c);
+        lds_barrier();
+        if (b + PF < nb) request(b + PF, slot_c);
+        if (b + PF + 1 < nb) lookup(b + PF + 1, std::integral_constant<int, (SL + 1) % PF>{});
+        if (busy) compute(b);
+    };
+    lookup(0, std::integral_constant<int, 0>{});
+    if constexpr (PF > 1) if (1 < nb) lookup(1, std::integral_constant<int, 1 % PF>{});
+    if constexpr (PF > 2) if (2 < nb) lookup(2, std::integral_constant<int, 2 % PF>{});
+    if (0 < nb) request(0, std::integral_constant<int, 0>{});
+    if constexpr (PF > 1) if (1 < nb) request(1, std::integral_constant<int, 1 % PF>{});
+    if constexpr (PF > 2) if (2 < nb) request(2, std::integral_constant<int, 2 % PF>{});
+    if (PF < nb) lookup(PF, std::integral_constant<int, 0>{});
+    int b = 0;
+    for (; b + PF <= nb; b += PF) {
+        iter(b, std::integral_constant<int, 0>{});
+        if constexpr (PF > 1) iter(b + 1, std::integral_constant<int, 1 % PF>{});
+        if constexpr (PF > 2) iter(b + 2, std::integral_constant<int, 2 % PF>{});
     }
+    if (b < nb) iter(b, std::integral_constant<int, 0>{});
+    if constexpr (PF > 2) if (b + 1 < nb) iter(b + 1, std::integral_constant<int, 1 % PF>{});
     if (!busy) return;
 
     const int64_t item_id = (int64_t)seq * a.h_kv + hk;
@@ -1031,33 +1068,42 @@ int dispatch_attn(const AttnArgs &a, int QT, int64_t n_items, hipStream_t st) {
 }
 
 template <int KT>
-int dispatch_attn_shared(const AttnArgs &a, int64_t n_items, hipStream_t st) {
-#define VX_SCASE(d)                                                                                              \
-    if (a.D == d) {                                                                                              \
-        hipLaunchKernelGGL((paged_attn_shared_kernel<KT, d>), dim3((unsigned)n_items), dim3(64 * kSharedWaves), 0, \
-                           st, a.bt, a.cu, a.kvo, a.n_splits, a.h_kv, a.max_blocks, a.chunk, a.ps, a);           \
-        return 0;                                                                                                \
+int dispatch_attn_shared(const AttnArgs &a, int pf, int64_t n_items, hipStream_t st) {
+#define VX_SCASE(d, p)                                                                                     \
+    if (a.D == d && pf == p) {                                                                             \
+        hipLaunchKernelGGL((paged_attn_shared_kernel<KT, d, p>), dim3((unsigned)n_items),                  \
+                           dim3(64 * kSharedWaves), 0, st, a.bt, a.cu, a.kvo, a.n_splits, a.h_kv,          \
+                           a.max_blocks, a.chunk, a.ps, a);                                                \
+        return 0;                                                                                          \
     }
-    VX_SCASE(32) VX_SCASE(64) VX_SCASE(128) VX_SCASE(256)
+    VX_SCASE(32, 1) VX_SCASE(64, 1) VX_SCASE(128, 1) VX_SCASE(256, 1)
 #undef VX_SCASE
     return set_error("paged_attention: no kernel for head_dim");
 }
 
 // The shared-KV kernel takes a sequence's query vectors when they exceed one
 // 32-vector tile and fit its eight waves (mode 0, 16-bit, no fused qkv
-// finish); VX_ATTN_SHARED=0 turns it off.
-bool use_shared_attn(int mode, int64_t max_rows, int64_t G, int64_t D) {
+// finish), for power-of-two page sizes and pools of fewer than 2^31 elements;
+// VX_ATTN_SHARED=0 turns it off.
+bool use_shared_attn(int mode, int64_t max_rows, int64_t G, int64_t D, int64_t ps, int64_t pool_elems) {
     const char *env = getenv("VX_ATTN_SHARED");
     if (env && env[0] == '0') return false;
     const int64_t v = max_rows * G;
-    return mode == 0 && v > 32 && v <= kSharedNV && (D == 32 || D == 64 || D == 128 || D == 256);
+    return mode == 0 && v > 32 && v <= kSharedNV && (D == 32 || D == 64 || D == 128 || D == 256) && ps > 0 &&
+           (ps & (ps - 1)) == 0 && pool_elems < (1ll << 31);
 }
 
-// Its KV split: ~2 workgroups per CU (one at D = 256, whose LDS fills a CU),
-// at least two key blocks per split.  VX_ATTN_SHARED_SPLITS overrides the count.
-void shared_attn_plan(int64_t base_items, int64_t max_kv, int64_t D, int64_t &splits, int64_t &chunk) {
+// Its prefetch depth: one key block in flight in registers, two workgroups
+// per CU (D <= 128).  Deeper rings (two or three blocks, one workgroup per
+// CU for the registers) measured slower on config 3's tree step.
+int shared_attn_depth(int64_t) { return 1; }
+
+// Its KV split: ~2 workgroups per CU at depth 1 with D <= 128 (one otherwise:
+// the registers or, at D = 256, the LDS fill a CU), at least two key blocks
+// per split.  VX_ATTN_SHARED_SPLITS overrides the count.
+void shared_attn_plan(int64_t base_items, int64_t max_kv, int64_t D, int pf, int64_t &splits, int64_t &chunk) {
     const int64_t max_keys = std::max<int64_t>(1, max_kv);
-    const int64_t per_cu = D <= 128 ? 2 : 1;
+    const int64_t per_cu = D <= 128 && pf == 1 ? 2 : 1;
     splits = std::max<int64_t>(1, per_cu * device_cu_count() / std::max<int64_t>(1, base_items));
     const char *env = getenv("VX_ATTN_SHARED_SPLITS");
     if (env && *env) splits = std::max(1, atoi(env));
@@ -1083,7 +1129,7 @@ size_t attn_workspace_bound(int64_t n_seqs, int64_t h_kv, int64_t max_rows, int6
     const int64_t nqt = vx_cdiv(max_rows, qr);
     const int64_t splits = std::max<int64_t>(1, vx_cdiv(max_kv, 2 * kKeyBlock));
     size_t need = attn_workspace_bytes(n_seqs, h_kv, nqt, splits, D);
-    if (use_shared_attn(0, max_rows, G, D) && splits > 1)
+    if (use_shared_attn(0, max_rows, G, D, 1, 0) && splits > 1)
         need = std::max(need, kAttnCounterBytes + (size_t)n_seqs * h_kv * splits * kSharedNV * (2 + D) * 4);
     return need;
 }
@@ -1141,11 +1187,12 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
         return 0;
     }
     a.pnv = 64;
-    if (use_shared_attn(mode, max_rows, a.G, D) && !fuse) {
+    if (use_shared_attn(mode, max_rows, a.G, D, ps, num_pages * h_kv * ps * D) && !fuse) {
         // one workgroup per (sequence, KV head, split) over all query vectors
         const int64_t base_items = n_seqs * h_kv;
         int64_t splits, chunk;
-        shared_attn_plan(base_items, max_kv, D, splits, chunk);
+        const int pf = shared_attn_depth(D);
+        shared_attn_plan(base_items, max_kv, D, pf, splits, chunk);
         a.n_qtiles = 1;
         a.qr = (int)max_rows;
         a.pnv = kSharedNV;
@@ -1162,8 +1209,8 @@ int paged_attention_launch(const void *q, const void *k_pool, const void *v_pool
         }
         a.partial = ws ? (float *)((char *)ws + kAttnCounterBytes) : nullptr;
         const int64_t n_items = base_items * splits;
-        int rc = dtype == VX_F16 ? dispatch_attn_shared<VX_F16>(a, n_items, st)
-                                 : dispatch_attn_shared<VX_BF16>(a, n_items, st);
+        int rc = dtype == VX_F16 ? dispatch_attn_shared<VX_F16>(a, pf, n_items, st)
+                                 : dispatch_attn_shared<VX_BF16>(a, pf, n_items, st);
         if (rc) return rc;
         if (splits > 1) launch_combine(a, dtype, base_items, (int)std::min<int64_t>(kSharedNV, max_rows * a.G), st);
         VX_HIP(hipGetLastError());
