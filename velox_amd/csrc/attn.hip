@@ -862,6 +862,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 &&
     if constexpr (PF > 2) if (b + 1 < nb) iter(b + 1, std::integral_constant<int, 1 % PF>{});
     if (!busy) return;
 
+    if (!qlive) return;  // the merge reads live vectors only
     const int64_t item_id = (int64_t)seq * a.h_kv + hk;
     if (n_splits_arg > 1) {
         // partial layout per (item, split): m[NV], l[NV], O[NV][D]
@@ -876,7 +877,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 &&
                 make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
         return;
     }
-    if (!qlive) return;
     const float inv = 1.0f / l_run;
 #pragma unroll
     for (int i = 0; i < DT; i++) {
