@@ -571,6 +571,20 @@ def test_shared_kv_attention_tree_bf16(cuda, monkeypatch, splits):
     assert_allclose_elementwise("shared-kv tree bf16", got, ref, 3e-2, 3e-2)
 
 
+def test_shared_kv_attention_page_size_fallback(cuda):
+    """A page size that is not a power of two (24) sends 68-vector sequences
+    to the query-tile kernel instead; the 4-2-2 tree still matches the
+    oracle."""
+    par = tree_4_2_2()
+    R, B, ps = len(par), 3, 24
+    offs = [40, 101, 7]
+    nb = (max(offs) + R + ps - 1) // ps
+    rng = np.random.default_rng(24)
+    perm = rng.permutation(B * nb + 1)[: B * nb].reshape(B, nb)
+    got, ref = _prefill_case([R] * B, offs, perm, B * nb + 1, 23, dt="f16", hq=32, hk=8, ps=ps, tree=par)
+    assert_allclose_elementwise("page size 24 tree", got, ref, 1e-2, 1e-2)
+
+
 def test_shared_kv_attention_sliding_window(cuda):
     """Window 16 over 12 rows x 4 query heads (48 vectors, the shared-KV
     kernel) at kv_offset 80: matches the oracle and differs from the global
