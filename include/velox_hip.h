@@ -102,7 +102,10 @@ int vx_qmm_4bit_packed(const void *x, const void *packed, void *y, const void *r
  * uint64 [total_q] or NULL): row t of a sequence sees context positions
  * < kv_offset and tree slot kv_offset + j iff bit j is set; NULL keeps the
  * reference's causal rule (kv_len = kv_offset + t + 1).  q/k/v/out share
- * dtype.  Requires head_dim % 32 == 0, head_dim <= 256, h_q % h_kv == 0. */
+ * dtype.  Requires head_dim % 32 == 0, head_dim <= 256, h_q % h_kv == 0.
+ * cu_seqlens, seq_id_per_q and kv_offsets are read back on the host (one
+ * small copy and a stream synchronisation) to check the rows and size the
+ * launch; KV-split partials use the per-stream library workspace. */
 int vx_paged_attention(const void *q, const void *k_pool, const void *v_pool,
                        const uint32_t *block_table, const uint32_t *cu_seqlens,
                        const uint32_t *seq_id_per_q, const uint32_t *kv_offsets,
