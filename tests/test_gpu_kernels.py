@@ -571,6 +571,20 @@ def test_shared_kv_attention_tree_bf16(cuda, monkeypatch, splits):
     assert_allclose_elementwise("shared-kv tree bf16", got, ref, 3e-2, 3e-2)
 
 
+def test_shared_kv_attention_empty_sequence(cuda, monkeypatch):
+    """A sequence with no rows between two that take the shared-KV kernel:
+    its workgroups leave before any barrier and the merge skips it."""
+    monkeypatch.setenv("VX_ATTN_SHARED_SPLITS", "3")
+    rows, ps = [17, 0, 9], 16
+    offs = [300, 50, 333]
+    nb = (max(o + r for o, r in zip(offs, rows)) + ps - 1) // ps
+    rng = np.random.default_rng(7)
+    P = 3 * nb + 1
+    perm = rng.permutation(P)[: 3 * nb].reshape(3, nb)
+    got, ref = _prefill_case(rows, offs, perm, P, 29, dt="f16", hq=8, hk=2, d=128)
+    assert_allclose_elementwise("shared-kv empty sequence", got, ref, 1e-2, 1e-2)
+
+
 def test_shared_kv_attention_page_size_fallback(cuda):
     """A page size that is not a power of two (24) sends 68-vector sequences
     to the query-tile kernel instead; the 4-2-2 tree still matches the
