@@ -897,7 +897,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 &&
 // a partial holds a.pnv vectors: m[pnv], l[pnv], O[pnv][D].  One thread per
 // (tile, vector, four consecutive d), nv vectors per tile; the splits'
 // statistics and values are requested eight splits at a time, so a merge of
-// up to eight splits costs two memory round trips.
+// up to eight splits costs one memory round trip.
 template <int KT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int nv) {
     constexpr int kB = 8;
@@ -923,19 +923,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int nv) {
     const int64_t tile_id = ((int64_t)seq * a.h_kv + hk) * a.n_qtiles + qtile;
     const int64_t stride = (int64_t)a.pnv * (2 + a.D);
     const float *p0 = a.partial + tile_id * a.n_splits * stride;
-    float M = -__builtin_inff();
-    for (int s0 = 0; s0 < a.n_splits; s0 += kB) {
-        float mb[kB];
-#pragma unroll
-        for (int j = 0; j < kB; j++) mb[j] = s0 + j < a.n_splits ? p0[(s0 + j) * stride + n] : -__builtin_inff();
-#pragma unroll
-        for (int j = 0; j < kB; j++) M = fmaxf(M, mb[j]);
-    }
     float L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < a.n_splits; s0 += kB) {
-        float mb[kB], lb[kB];
-        float4 ob[kB];
+    auto load_batch = [&](int s0, float (&mb)[kB], float (&lb)[kB], float4 (&ob)[kB]) {
 #pragma unroll
         for (int j = 0; j < kB; j++) {
             const bool ok = s0 + j < a.n_splits;
@@ -944,6 +934,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int nv) {
             lb[j] = ok ? ps[a.pnv + n] : 0.f;
             ob[j] = ok ? *(const float4 *)(ps + 2 * a.pnv + (int64_t)n * a.D + d) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+    };
+    auto add_batch = [&](int s0, float M, const float (&mb)[kB], const float (&lb)[kB], const float4 (&ob)[kB]) {
 #pragma unroll
         for (int j = 0; j < kB; j++) {
             if (s0 + j >= a.n_splits) break;
@@ -953,6 +945,32 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int nv) {
             acc.y += ob[j].y * f;
             acc.z += ob[j].z * f;
             acc.w += ob[j].w * f;
+        }
+    };
+    if (a.n_splits <= kB) {
+        // one batch: the maximum comes from the loaded statistics
+        float mb[kB], lb[kB];
+        float4 ob[kB];
+        load_batch(0, mb, lb, ob);
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < kB; j++) M = fmaxf(M, mb[j]);
+        add_batch(0, M, mb, lb, ob);
+    } else {
+        // the maximum first, then the sum in split order, eight splits a batch
+        float M = -__builtin_inff();
+        for (int s0 = 0; s0 < a.n_splits; s0 += kB) {
+            float mb[kB];
+#pragma unroll
+            for (int j = 0; j < kB; j++) mb[j] = s0 + j < a.n_splits ? p0[(s0 + j) * stride + n] : -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < kB; j++) M = fmaxf(M, mb[j]);
+        }
+        for (int s0 = 0; s0 < a.n_splits; s0 += kB) {
+            float mb[kB], lb[kB];
+            float4 ob[kB];
+            load_batch(s0, mb, lb, ob);
+            add_batch(s0, M, mb, lb, ob);
         }
     }
     const float vals[4] = {acc.x / L, acc.y / L, acc.z / L, acc.w / L};
