@@ -541,18 +541,6 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const uint32_t *bt_arg,
     }
 }
 
-// Shared-KV attention: one workgroup per (sequence, KV head, KV split) holds
-// all of the item's query vectors (its rows x G query heads, up to 128).  The
-// eight waves stage each 64-key block once in LDS -- K row-major with its
-// 16-byte chunks XOR-swizzled by row, V transposed (d-major, keys in pairs
-// per 32-bit word) -- and wave w runs query tile w (vectors 16 w .. 16 w + 15)
-// over every block of the range, with the S^T / P^T / O^T fragment layouts of
-// paged_attn_kernel.  The tiled kernel reads an item's KV range once per
-// query tile; a 17-node tree with 4 query heads per KV head has 68 vectors,
-// i.e. three 32-vector tiles and three reads.  Block b + 1 is requested into
-// registers while block b is computed, and the block table one block ahead
-// of that.  Keys past the range are staged as zeros.  Splits publish
-// (m, l, O) for attn_combine_kernel with kSharedNV vectors per partial.
 // Workgroup barrier that orders LDS only: __syncthreads() is also a release
 // of global memory, i.e. a vmcnt(0) wait, which would drain the key blocks
 // requested ahead of it.
@@ -562,6 +550,20 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Shared-KV attention: one workgroup per (sequence, KV head, KV split) holds
+// all of the item's query vectors (its rows x G query heads, up to 128).  The
+// eight waves stage each 64-key block once in LDS -- K row-major with its
+// 16-byte chunks XOR-swizzled by row, V transposed (d-major, keys in pairs
+// per 32-bit word) -- and wave w runs query tile w (vectors 16 w .. 16 w + 15)
+// over every block of the range, with the S^T / P^T / O^T fragment layouts of
+// paged_attn_kernel.  The tiled kernel reads an item's KV range once per
+// query tile; a 17-node tree with 4 query heads per KV head has 68 vectors,
+// i.e. three 32-vector tiles and three reads.  Blocks b + 1 .. b + PF are
+// requested into a PF-slot register ring while block b is computed, and the
+// block table one block ahead of that; the launcher instantiates PF = 1
+// (deeper rings need one workgroup per CU for their registers and measured
+// slower).  Keys past the range are staged as zeros.  Splits publish
+// (m, l, O) for attn_combine_kernel with kSharedNV vectors per partial.
 constexpr int kSharedWaves = 8;
 constexpr int kSharedNV = kSharedWaves * 16;
 
@@ -571,10 +573,10 @@ constexpr size_t attn_shared_lds_bytes() {
 }
 
 template <int KT, int D, int PF>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 && PF == 1 ? 4 : 2))) void paged_attn_shared_kernel(const uint32_t *bt_arg, const uint32_t *cu_arg,
-                                                                const uint32_t *kvo_arg, int n_splits_arg,
-                                                                int h_kv_arg, int max_blocks_arg, int chunk_arg,
-                                                                int ps_arg, AttnArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D <= 128 && PF == 1 ? 4 : 2)))
+void paged_attn_shared_kernel(const uint32_t *bt_arg, const uint32_t *cu_arg, const uint32_t *kvo_arg,
+                              int n_splits_arg, int h_kv_arg, int max_blocks_arg, int chunk_arg, int ps_arg,
+                              AttnArgs a) {
     typedef typename MfmaT<KT>::frag frag;
     constexpr int DK = D / 32;               // MFMA k-steps over head_dim
     constexpr int DT = D / 16;               // output row tiles of O^T
